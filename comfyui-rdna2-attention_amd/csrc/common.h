@@ -1,0 +1,88 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels.
+//
+// All sources are compiled with -ffp-contract=off: a multiply and an add stay two
+// IEEE operations unless the code calls __builtin_fmaf, so every rounding point
+// is explicit and the CPU oracle can restate it bit for bit. fp32 division and
+// square root are correctly rounded (hipcc's default), and fp32 denormals are kept.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef int i16v __attribute__((ext_vector_type(16)));
+typedef unsigned u32;
+typedef u32 u2v __attribute__((ext_vector_type(2)));
+typedef u32 u4v __attribute__((ext_vector_type(4)));
+
+#define RDA_ERR_INVALID 1  // hipErrorInvalidValue
+
+// Rounds an fp32 value to fp16 and back (one RNE rounding).
+__device__ __forceinline__ float r16(float x) { return (float)(half_t)x; }
+
+// exp(x): 2^n e^r with n = rint(x log2 e), r = x - n ln2 by a two-constant
+// Cody-Waite reduction, e^r by a degree-7 Taylor polynomial in Horner form, and
+// 2^n as two exact power-of-two factors. Below -88 it returns 0 (1 + e^x == 1
+// there), above ln(FLT_MAX) +inf. Every step is an IEEE fp32 operation, so the
+// CPU restatement reproduces it exactly.
+__device__ __forceinline__ float pow2i(int n) { return __int_as_float((n + 127) << 23); }
+__device__ __forceinline__ float scale2(float p, int n) {
+    const int h = n / 2;
+    return (p * pow2i(h)) * pow2i(n - h);
+}
+__device__ __forceinline__ float rda_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -88.0f) return 0.0f;
+    const float n = rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723e-6f, r);
+    float p = 1.98412701138295233e-4f;
+    p = __builtin_fmaf(p, r, 1.38888892251998186e-3f);
+    p = __builtin_fmaf(p, r, 8.33333376795053482e-3f);
+    p = __builtin_fmaf(p, r, 4.16666679084300995e-2f);
+    p = __builtin_fmaf(p, r, 1.66666671633720398e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return scale2(p, (int)n);
+}
+// 2^y = 2^n 2^f with n = rint(y), f = y - n (exact), 2^f by the polynomial of
+// e^(f ln 2) with its coefficients multiplied through by powers of ln 2.
+__device__ __forceinline__ float rda_exp2f(float y) {
+    if (y != y) return y;
+    if (y >= 128.0f) return __builtin_inff();
+    if (y < -127.0f) return 0.0f;
+    const float n = rintf(y);
+    const float f = y - n;
+    float p = 1.52527336467755958e-5f;
+    p = __builtin_fmaf(p, f, 1.54035296873189509e-4f);
+    p = __builtin_fmaf(p, f, 1.33335578721016645e-3f);
+    p = __builtin_fmaf(p, f, 9.61812864989042282e-3f);
+    p = __builtin_fmaf(p, f, 5.55041097104549408e-2f);
+    p = __builtin_fmaf(p, f, 2.40226507186889648e-1f);
+    p = __builtin_fmaf(p, f, 6.93147182464599609e-1f);
+    p = __builtin_fmaf(p, f, 1.0f);
+    return scale2(p, (int)n);
+}
+
+// Wave64 reductions. xor shuffles of width 64 stay exact for max; sums are
+// evaluated in the butterfly order (lane values paired at distance 32, 16, ...).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ i4v as_i4(u4v v) { return __builtin_bit_cast(i4v, v); }

@@ -1,0 +1,296 @@
+// Single-token (decode) kernels: the ConvRot rotation of one activation row, the int8 and bf16
+// GEMVs that read the weights straight from their stored form, and split-K GQA attention over a
+// fixed-capacity KV cache. One row of activations makes the linears purely HBM-bound: weights
+// are streamed once with 16-byte non-temporal loads, the activation row sits in LDS.
+#include "common.h"
+
+#define GV_WAVES 4
+#define SPLITS 32  // position chunks per (batch, kv head) in attn_decode
+#define HEAD 128
+
+// rotate (int8_gemv.hip:31-52): H4 steps at strides 1, 4, 16, ... < group in fp32, times 1/sqrt(group).
+__global__ __launch_bounds__(256) void rotate_kernel(const float* __restrict__ x, float* __restrict__ out, int group) {
+    extern __shared__ float s[];
+    const float* in = x + (size_t)blockIdx.x * group;
+    for (int i = threadIdx.x; i < group; i += 256) s[i] = in[i];
+    __syncthreads();
+    for (int stride = 1; stride < group; stride *= 4) {
+        for (int q = threadIdx.x; q < group / 4; q += 256) {
+            const int i = (q / stride) * stride * 4 + q % stride;
+            const float a = s[i], b = s[i + stride], c = s[i + stride * 2], d = s[i + stride * 3];
+            const float sum = a + b + c + d;
+            s[i] = sum - 2.0f * d;
+            s[i + stride] = sum - 2.0f * c;
+            s[i + stride * 2] = sum - 2.0f * b;
+            s[i + stride * 3] = sum - 2.0f * a;
+        }
+        __syncthreads();
+    }
+    const float norm = 1.0f / sqrtf((float)group);
+    float* o = out + (size_t)blockIdx.x * group;
+    for (int i = threadIdx.x; i < group; i += 256) o[i] = s[i] * norm;
+}
+
+__device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
+
+// out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns RW rows
+// and walks them together in steps of 1024 values (16 per lane; a last half step of 512 when
+// K % 1024 == 512), so one LDS read of x feeds RW rows. x is fp32 or fp16; out has the dtype of x.
+// x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses:
+// the f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
+template <int RW, bool XH>
+__global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
+                                                                 const float* __restrict__ bias, void* __restrict__ out, int N, int K) {
+    extern __shared__ f4 xs[];
+    const int steps = K / 1024;
+    for (int i = threadIdx.x; i < K / 4; i += GV_WAVES * 64) {
+        f4 v;
+        if (XH) {
+            const h4v hv = ((const h4v*)xin)[i];
+            v = (f4){(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
+        } else {
+            v = ((const f4*)xin)[i];
+        }
+        const int tail = i - steps * 256;
+        xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = v;
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * GV_WAVES + wave) * RW;
+    if (row >= N) return;
+    const int8_t* base = w + (size_t)row * K;
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = 0.f;
+    for (int s = 0; s < steps; s++) {
+        u4v v[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) v[r] = __builtin_nontemporal_load((const u4v*)(base + (size_t)r * K + s * 1024 + lane * 16));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f4 xv = xs[(s * 4 + j) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[r][j], i), xv[i], acc[r]);
+        }
+    }
+    if (K % 1024) {
+        const int k0 = steps * 1024 + lane * 8;
+        u2v v[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) v[r] = __builtin_nontemporal_load((const u2v*)(base + (size_t)r * K + k0));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const f4 xv = xs[steps * 256 + j * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[r][j], i), xv[i], acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        float sum = wave_sum(acc[r]) * scale[row + r];
+        if (bias) sum = sum + bias[row + r];
+        if (lane == 0) {
+            if (XH) ((half_t*)out)[row + r] = (half_t)sum;
+            else ((float*)out)[row + r] = sum;
+        }
+    }
+}
+
+// logits[n] = sum_k bf16(w[n, k]) x[k] (int8_gemv.hip:87-119): 8 weights per lane per step of 512, a
+// last half step of 256 when K % 512 == 256.
+__device__ __forceinline__ float bf16_dot4(u32 a, u32 b, f4 xv, float acc) {
+    acc = __builtin_fmaf(__uint_as_float(a << 16), xv[0], acc);
+    acc = __builtin_fmaf(__uint_as_float(a & 0xffff0000u), xv[1], acc);
+    acc = __builtin_fmaf(__uint_as_float(b << 16), xv[2], acc);
+    return __builtin_fmaf(__uint_as_float(b & 0xffff0000u), xv[3], acc);
+}
+
+template <int RW>
+__global__ __launch_bounds__(GV_WAVES * 64) void gemv_bf16_kernel(const float* __restrict__ x, const u32* __restrict__ w, float* __restrict__ out, int N,
+                                                                  int K) {
+    extern __shared__ f4 xs[];
+    const int steps = K / 512;
+    // Reading order: f4 j of lane l in step s at (2s + j) * 64 + l; the half step's f4 of lane l at 128 steps + l.
+    for (int i = threadIdx.x; i < K / 4; i += GV_WAVES * 64) {
+        const int tail = i - steps * 128;
+        xs[tail < 0 ? ((i >> 7) * 2 + (i & 1)) * 64 + ((i & 127) >> 1) : steps * 128 + tail] = ((const f4*)x)[i];
+    }
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = (blockIdx.x * GV_WAVES + wave) * RW;
+    if (row >= N) return;
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) acc[r] = 0.f;
+    for (int s = 0; s < steps; s++) {
+        u4v v[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) v[r] = __builtin_nontemporal_load((const u4v*)(w + ((size_t)(row + r) * K + s * 512 + lane * 8) / 2));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const f4 xv = xs[(s * 2 + j) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < RW; r++) acc[r] = bf16_dot4(v[r][j * 2], v[r][j * 2 + 1], xv, acc[r]);
+        }
+    }
+    if (K % 512) {
+        const int k0 = steps * 512 + lane * 4;
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const u2v v = __builtin_nontemporal_load((const u2v*)(w + ((size_t)(row + r) * K + k0) / 2));
+            acc[r] = bf16_dot4(v[0], v[1], xs[steps * 128 + lane], acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const float sum = wave_sum(acc[r]);
+        if (lane == 0) out[row + r] = sum;
+    }
+}
+
+// attn_decode (int8_gemv.hip:121-180): one new token over the cache, split by position so that a few
+// KV heads still fill the GPU. The grid is fixed and the length is read here, so a captured graph
+// stays valid as the cache grows. A wave takes one position at a time: a K or V row of a head is
+// 512 bytes, 8 per lane, shared by the REP query heads of the KV head.
+template <int REP>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                                                          const int* __restrict__ lengths, float* __restrict__ partial, float* __restrict__ stats,
+                                                          int capacity, int kv_heads, float scale) {
+    constexpr int W = 4;
+    __shared__ float acc_s[W][REP][HEAD];
+    __shared__ float max_s[W][REP], sum_s[W][REP];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.y / kv_heads, kv_head = blockIdx.y % kv_heads, split = blockIdx.x;
+    const int length = lengths[b];
+    const int chunk = (length + SPLITS - 1) / SPLITS;
+    const int end = min((split + 1) * chunk, length);
+    const int first_head = (b * kv_heads + kv_head) * REP;
+
+    f2 qv[REP], acc[REP];
+    float mx[REP], sum[REP];
+#pragma unroll
+    for (int g = 0; g < REP; g++) {
+        qv[g] = ((const f2*)(q + (size_t)(first_head + g) * HEAD))[lane] * scale;
+        acc[g] = (f2){0.f, 0.f};
+        mx[g] = -1e30f;
+        sum[g] = 0.f;
+    }
+    for (int j = split * chunk + wave; j < end; j += W) {
+        const size_t row = ((size_t)(b * capacity + j) * kv_heads + kv_head) * HEAD;
+        const f2 kv = ((const f2*)(k + row))[lane], vv = ((const f2*)(v + row))[lane];
+#pragma unroll
+        for (int g = 0; g < REP; g++) {
+            const f2 d = qv[g] * kv;
+            const float score = wave_sum(d[0] + d[1]);
+            const float next = fmaxf(mx[g], score);
+            const float keep = expf(mx[g] - next), p = expf(score - next);
+            sum[g] = sum[g] * keep + p;
+            acc[g] = acc[g] * keep + vv * p;
+            mx[g] = next;
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < REP; g++) {
+        ((f2*)acc_s[wave][g])[lane] = acc[g];
+        if (lane == 0) {
+            max_s[wave][g] = mx[g];
+            sum_s[wave][g] = sum[g];
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < REP * HEAD; i += 256) {
+        const int g = i / HEAD, d = i % HEAD;
+        float top = max_s[0][g];
+#pragma unroll
+        for (int w = 1; w < W; w++) top = fmaxf(top, max_s[w][g]);
+        float value = 0.f, total = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const float keep = expf(max_s[w][g] - top);
+            value += acc_s[w][g][d] * keep;
+            total += sum_s[w][g] * keep;
+        }
+        const size_t at = (size_t)(first_head + g) * SPLITS + split;
+        partial[at * HEAD + d] = value;
+        if (d == 0) {
+            stats[at * 2] = top;
+            stats[at * 2 + 1] = total;
+        }
+    }
+}
+
+// attn_merge (int8_gemv.hip:182-195): joins the splits, one block per query head.
+__global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restrict__ partial, const float* __restrict__ stats, float* __restrict__ out) {
+    const size_t head = blockIdx.x;
+    const float* st = stats + head * SPLITS * 2;
+    float top = st[0];
+    for (int s = 1; s < SPLITS; s++) top = fmaxf(top, st[s * 2]);
+    float value = 0.f, total = 0.f;
+    for (int s = 0; s < SPLITS; s++) {
+        const float keep = expf(st[s * 2] - top);
+        value += partial[(head * SPLITS + s) * HEAD + threadIdx.x] * keep;
+        total += st[s * 2 + 1] * keep;
+    }
+    out[head * HEAD + threadIdx.x] = value / total;
+}
+
+template <int RW, bool XH>
+static int launch_gemv(const void* x, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
+    const int rows = GV_WAVES * RW;
+    hipLaunchKernelGGL((gemv_i8_kernel<RW, XH>), dim3((N + rows - 1) / rows), dim3(GV_WAVES * 64), (size_t)K * 4, (hipStream_t)stream, x,
+                       (const int8_t*)w, scale, bias, out, N, K);
+    return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
+    if (rows <= 0 || group < 4 || group > 16384 || (group & (group - 1)) != 0 || (__builtin_ctz(group) & 1)) return RDA_ERR_INVALID;
+    hipLaunchKernelGGL(rotate_kernel, dim3(rows), dim3(256), (size_t)group * 4, (hipStream_t)stream, x, out, group);
+    return (int)hipGetLastError();
+}
+
+// x_half: 0 for fp32 x and out, 1 for fp16 x and out.
+int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
+    if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384 || N % 4 != 0) return RDA_ERR_INVALID;
+    // Enough rows per wave to amortise the x staging, few enough that every CU gets work.
+    const bool many = N >= 4096 && N % (GV_WAVES * 4) == 0;
+    if (x_half) return many ? launch_gemv<4, true>(x, w, scale, bias, out, N, K, stream) : launch_gemv<1, true>(x, w, scale, bias, out, N, K, stream);
+    return many ? launch_gemv<4, false>(x, w, scale, bias, out, N, K, stream) : launch_gemv<1, false>(x, w, scale, bias, out, N, K, stream);
+}
+
+int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream) {
+    if (N <= 0 || K <= 0 || K % 256 != 0 || K > 16384 || N % (GV_WAVES * 2) != 0) return RDA_ERR_INVALID;
+    hipLaunchKernelGGL(gemv_bf16_kernel<2>, dim3(N / (GV_WAVES * 2)), dim3(GV_WAVES * 64), (size_t)K * 4, (hipStream_t)stream, x, (const u32*)w, out, N,
+                       K);
+    return (int)hipGetLastError();
+}
+
+int rda_attn_decode(const float* q, const float* k, const float* v, const int* lengths, float* partial, float* stats, int B, int H, int Hkv,
+                    int capacity, float scale, void* stream) {
+    if (B <= 0 || Hkv <= 0 || H % Hkv != 0 || capacity <= 0) return RDA_ERR_INVALID;
+    const int rep = H / Hkv;
+    dim3 grid(SPLITS, B * Hkv);
+    switch (rep) {
+    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    default: return RDA_ERR_INVALID;
+    }
+    return (int)hipGetLastError();
+}
+
+int rda_attn_merge(const float* partial, const float* stats, float* out, int heads, void* stream) {
+    if (heads <= 0) return RDA_ERR_INVALID;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(heads), dim3(HEAD), 0, (hipStream_t)stream, partial, stats, out);
+    return (int)hipGetLastError();
+}
+
+int rda_decode_splits(void) { return SPLITS; }
+
+}  // extern "C"

@@ -1,0 +1,283 @@
+// Activation -> block Hadamard ("ConvRot") rotation -> per-token absmax quantization, one pass.
+//
+// One 256-thread workgroup (four wave64s) owns one row. A rotation group is split over
+// lanes that each hold 16 consecutive values: the two fastest base-4 digits are H4 steps
+// in registers, an LDS transpose per group brings the remaining digits into registers,
+// and the rotated fp16 row stays in LDS until the row's absmax is known. The int8 codes
+// are written row-major [M, K], which is what the GEMM's LDS stage reads.
+//
+// Arithmetic follows rot_quant (int8_gemm.hip:151-243) step for step: fp32 butterflies
+// in digit order 1, 4, 16, 64, times 1/16, rounded to fp16, absmax over the fp16 values,
+// scale = max(absmax / 127, 1e-30), q = clamp(floor(x / scale + 0.5), -128, 127).
+#include "common.h"
+
+enum Act { NO_ACT = 0, SITU = 1, SWIGLU = 2, GATE = 3, MOD = 4 };
+struct ModArgs {
+    const float* w;
+    const half_t* s;
+    const half_t* t;
+    int L;
+    float eps;
+};
+
+#define QT 256  // threads per row
+
+// int8_gemm.hip:106-109
+__device__ __forceinline__ void h4(float& a, float& b, float& c, float& d) {
+    const float s = a + b + c + d, a0 = a, b0 = b;
+    a = s - 2.f * d;
+    b = s - 2.f * c;
+    c = s - 2.f * b0;
+    d = s - 2.f * a0;
+}
+__device__ __forceinline__ void h16(float (&v)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) h4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) h4(v[i], v[i + 4], v[i + 8], v[i + 12]);
+}
+
+// int8_gemm.hip:118-127, with the exponentials of common.h.
+__device__ __forceinline__ float soft_tanh(float x) {
+    const float ax = fabsf(x), t = rda_exp2f(-2.885390082f * ax);
+    float y = (1.f - t) / (1.f + t);
+    if (ax < 0.02f) y = ax * (1.f - ax * ax * (1.f / 3.f - ax * ax * (2.f / 15.f)));
+    return x < 0.f ? -y : y;
+}
+__device__ __forceinline__ float situ(float hidden, float gate) {
+    const float sigmoid = 1.f / (1.f + rda_exp2f(-1.442695041f * gate));
+    return r16(4.f * soft_tanh(gate * 0.25f) * sigmoid * 25.f * soft_tanh(hidden * 0.04f));
+}
+// int8_gemm.hip:130-132
+__device__ __forceinline__ float swiglu(float gate, float up) { return r16(r16(gate / (1.f + rda_expf(-gate))) * up); }
+// int8_gemm.hip:135-137
+__device__ __forceinline__ float sigmoid_gate(float x, float gate) { return r16(x * r16(1.f / (1.f + rda_expf(-gate)))); }
+// int8_gemm.hip:140-143
+__device__ __forceinline__ float modulate(float x, float rstd, float w, float s, float t) {
+    return r16(r16(r16(x * rstd * (w + 1.f)) * s) + t);
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
+    return (u32)(a & 255) | ((u32)(b & 255) << 8) | ((u32)(c & 255) << 16) | ((u32)(d & 255) << 24);
+}
+
+// GROUP 256 or 128 rotates; GROUP 0 is quant_pack_a (no rotation, int8_gemm.hip:93-103).
+template <int ACT, bool I4, int GROUP>
+__global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
+                                                       int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    __shared__ float red[8];
+    half_t* rotated = (half_t*)smem;
+    const int row = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const half_t* x = X + (size_t)row * ldx;
+    float mx = 0.f;
+
+    if constexpr (GROUP == 0) {
+        for (int i = t; i < K / 8; i += QT) {
+            const h8 v = ((const h8*)x)[i];
+            ((h8*)rotated)[i] = v;
+#pragma unroll
+            for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf((float)v[j]));
+        }
+    } else {
+        float rstd = 0.f;
+        if constexpr (ACT == MOD) {
+            // The sum of squares in rms_norm_row's order (rms_norm.hip:19-37): thread t adds its chunks
+            // t + 256c with FMAs, 32-lane butterflies, then the eight partial sums in order.
+            float sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = t + c * QT;
+                if (i < K / 8) {
+                    const h8 v = ((const h8*)x)[i];
+                    ((h8*)rotated)[i] = v;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) sum = __builtin_fmaf((float)v[j], (float)v[j], sum);
+                }
+            }
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+            if ((t & 31) == 0) red[t >> 5] = sum;
+            __syncthreads();
+            float total = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) total += red[i];
+            rstd = 1.f / sqrtf(total / (float)K + mod.eps);
+            __syncthreads();
+        }
+        constexpr int LPG = GROUP / 16;  // lanes per group, 16 values each
+        constexpr int GPW = 64 / LPG;    // groups per wave per pass
+        const int gl = lane / LPG, c = lane % LPG, groups = K / GROUP;
+        float* sw = (float*)(smem + (size_t)K * 2) + (wave * 64 + gl * LPG) * 17;
+        const size_t mrow = ACT == MOD ? (size_t)(row / mod.L) * K : 0;
+        const half_t* ms = ACT == MOD ? mod.s + mrow : nullptr;
+        const half_t* mt = ACT == MOD ? mod.t + mrow : nullptr;
+        const float norm = GROUP == 256 ? 0.0625f : 0.0883883461356163025f;
+
+        for (int g0 = wave * GPW; g0 < groups; g0 += 4 * GPW) {
+            const int g = g0 + gl;
+            const bool active = g < groups;
+            float v[16];
+            if (active) {
+                const int e0 = g * GROUP + c * 16;
+                const half_t* src = ACT == MOD ? rotated : x;
+                const h8 lo = *(const h8*)(src + e0), hi = *(const h8*)(src + e0 + 8);
+                if (ACT == SITU) {
+                    const h8 glo = *(const h8*)(x + K + e0), ghi = *(const h8*)(x + K + e0 + 8);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v[i] = situ((float)lo[i], (float)glo[i]);
+                        v[8 + i] = situ((float)hi[i], (float)ghi[i]);
+                    }
+                } else if (ACT == SWIGLU || ACT == GATE) {
+                    const half_t* u = U + (size_t)row * K;
+                    const h8 ulo = *(const h8*)(u + e0), uhi = *(const h8*)(u + e0 + 8);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v[i] = ACT == SWIGLU ? swiglu((float)lo[i], (float)ulo[i]) : sigmoid_gate((float)lo[i], (float)ulo[i]);
+                        v[8 + i] = ACT == SWIGLU ? swiglu((float)hi[i], (float)uhi[i]) : sigmoid_gate((float)hi[i], (float)uhi[i]);
+                    }
+                } else if (ACT == MOD) {
+                    const h8 slo = *(const h8*)(ms + e0), shi = *(const h8*)(ms + e0 + 8);
+                    const h8 tlo = *(const h8*)(mt + e0), thi = *(const h8*)(mt + e0 + 8);
+                    const f4* w = (const f4*)(mod.w + e0);
+                    const f4 w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+                    const float wv[16] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w, w3.x, w3.y, w3.z, w3.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v[i] = modulate((float)lo[i], rstd, wv[i], (float)slo[i], (float)tlo[i]);
+                        v[8 + i] = modulate((float)hi[i], rstd, wv[8 + i], (float)shi[i], (float)thi[i]);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v[i] = (float)lo[i];
+                        v[8 + i] = (float)hi[i];
+                    }
+                }
+                h16(v);  // digits at strides 1 and 4
+#pragma unroll
+                for (int i = 0; i < 16; i++) sw[c * 17 + i] = v[i];
+            }
+            wave_sync();
+            if (active) {
+                int e[16];
+                if (GROUP == 256) {
+                    // Lane c now holds elements c + 16i: digits at strides 16 and 64.
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        v[i] = sw[i * 17 + c];
+                        e[i] = i * 16 + c;
+                    }
+                    h16(v);
+                } else {
+                    // Lane c takes the columns c and c + 8 (elements c + 16i, c + 8 + 16i, i < 8):
+                    // an H4 over the stride-16 digit, then an H2 over the stride-64 digit.
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        v[i] = sw[i * 17 + c];
+                        v[8 + i] = sw[i * 17 + c + 8];
+                        e[i] = c + 16 * i;
+                        e[8 + i] = c + 8 + 16 * i;
+                    }
+#pragma unroll
+                    for (int b = 0; b < 16; b += 4) h4(v[b], v[b + 1], v[b + 2], v[b + 3]);
+#pragma unroll
+                    for (int b = 0; b < 16; b += 8)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float p = v[b + i], q = v[b + i + 4];
+                            v[b + i] = p + q;
+                            v[b + i + 4] = p - q;
+                        }
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const half_t y = (half_t)(v[i] * norm);
+                    rotated[g * GROUP + e[i]] = y;
+                    mx = fmaxf(mx, fabsf((float)y));
+                }
+            }
+            wave_sync();
+        }
+    }
+    mx = wave_max(mx);
+    __syncthreads();
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float scale = I4 ? fmaxf(mx, 1e-10f) / 7.f : fmaxf(mx / 127.f, 1e-30f);
+    if (t == 0) as[row] = scale;
+
+    int8_t* out = Aq + (size_t)row * K;
+    for (int ch = t; ch < K / 16; ch += QT) {
+        const h8 lo = ((const h8*)rotated)[ch * 2], hi = ((const h8*)rotated)[ch * 2 + 1];
+        int q[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float f = (float)(i < 8 ? lo[i] : hi[i - 8]);
+            if (I4) q[i] = (int)fminf(fmaxf(rintf(f / scale), -7.f), 7.f);  // int8_gemm.hip:84
+            else q[i] = (int)fminf(fmaxf(floorf(f / scale + 0.5f), -128.f), 127.f);  // int8_gemm.hip:53
+        }
+        u4v o;
+#pragma unroll
+        for (int d = 0; d < 4; d++) o[d] = pack4(q[d * 4], q[d * 4 + 1], q[d * 4 + 2], q[d * 4 + 3]);
+        *(u4v*)(out + ch * 16) = o;
+    }
+}
+
+template <int ACT, bool I4, int GROUP>
+static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
+    if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || K > 16384) return RDA_ERR_INVALID;
+    const size_t lds = (size_t)K * 2 + (GROUP ? 4 * 64 * 17 * sizeof(float) : 0);
+    hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP>), dim3(M), dim3(QT), lds, (hipStream_t)stream, (const half_t*)x, ldx,
+                       (const half_t*)u, (int8_t*)aq, as, K, mod);
+    return (int)hipGetLastError();
+}
+
+template <int ACT, bool I4>
+static int dispatch_group(int group, const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
+    if (group == 256) return launch_rot_quant<ACT, I4, 256>(x, ldx, u, aq, as, M, K, mod, stream);
+    if (group == 128) return launch_rot_quant<ACT, I4, 128>(x, ldx, u, aq, as, M, K, mod, stream);
+    return RDA_ERR_INVALID;
+}
+
+extern "C" {
+
+int rda_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, void* stream) {
+    return launch_rot_quant<NO_ACT, false, 0>(x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_rot_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<NO_ACT, false>(group, x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_situ_rot_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<SITU, false>(group, x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_swiglu_rot_quant_pack_a(const void* gate, const void* up, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<SWIGLU, false>(group, gate, K, up, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_gate_rot_quant_pack_a(const void* x, const void* gate, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<GATE, false>(group, x, K, gate, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_mod_rot_quant_pack_a(const void* x, void* a_q, float* a_scale, int M, int K, const float* w, const void* s, const void* t, int L,
+                             float eps, void* stream) {
+    if (L <= 0 || K > 8192) return RDA_ERR_INVALID;
+    return launch_rot_quant<MOD, false, 256>(x, K, nullptr, a_q, a_scale, M, K, ModArgs{w, (const half_t*)s, (const half_t*)t, L, eps}, stream);
+}
+
+int rda_rot_quant_pack_a_i4(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<NO_ACT, true>(group, x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+}  // extern "C"

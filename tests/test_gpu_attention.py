@@ -1,0 +1,113 @@
+"""Parity of the fused attention (fp16 and int8-QK) on the GPU against the oracle.
+
+fp16 attention has no bit-exact pin (the matrix cores' summation order and the hardware exp2 are not reproducible
+on the CPU), so it is held to a stated tolerance against the float64 closed form: |out - ref| <= ATOL + RTOL |ref|
+with ATOL = RTOL = 2e-3 (P is rounded to fp16 before PV, 2^-11 relative; the output to fp16). The int8-QK variant is
+checked against the closed form of its own quantized scores (the Q/K codes and int32 scores are exact) to the
+same tolerance, and its quantized K against the oracle bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from comfyui_rdna2_attention_amd import _lib, attention, hip_attention
+from helpers import gen
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 2e-3
+
+
+def qkv(B, H, Hkv, Lq, Lk, seed, D=128):
+    g = gen(seed)
+    q = torch.randn(B, H, Lq, D, generator=g).half()
+    k = torch.randn(B, Hkv, Lk, D, generator=g).half()
+    v = torch.randn(B, Hkv, Lk, D, generator=g).half()
+    return q, k, v
+
+
+def close(out, ref):
+    out = out.detach().cpu().float().numpy().astype(np.float64)
+    err = np.abs(out - ref)
+    bound = ATOL + RTOL * np.abs(ref)
+    assert np.all(err <= bound), f"max abs err {err.max():.3e}, worst excess {(err - bound).max():.3e}"
+
+
+@pytest.mark.parametrize("int8_qk", [False, True])
+@pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096)])
+def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
+    print(f"attention B={B} H={H} Hkv={Hkv} Lq={Lq} Lk={Lk} int8_qk={int8_qk}", flush=True)
+    q, k, v = qkv(B, H, Hkv, Lq, Lk, seed=Lq + Lk)
+    out = torch.empty(B, H, Lq, 128, dtype=torch.float16, device=dev)
+    scale = 128 ** -0.5
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, scale, int8_qk)
+    ref = (oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64)(q.numpy(), k.numpy(), v.numpy(), scale)
+    close(out, ref)
+
+
+def test_attention_matches_reference_loop(dev):
+    """Tighter: the reference's own loop restated in fp32 (lazy rescale, fp16 P) agrees with the kernel."""
+    q, k, v = qkv(1, 2, 2, 256, 700, seed=3)
+    out = torch.empty(1, 2, 256, 128, dtype=torch.float16, device=dev)
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5)
+    ref = oracle.attention_faithful(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5).astype(np.float64)
+    err = np.abs(out.cpu().float().numpy() - ref)
+    assert err.max() <= 1e-3
+
+
+def test_attention_large_scores(dev):
+    """Scores far above the lazy-rescale threshold (8 in log2 units): the running maximum must move."""
+    q, k, v = qkv(1, 2, 2, 200, 1200, seed=5)
+    q = (q.float() * 4).half()
+    out = torch.empty(1, 2, 200, 128, dtype=torch.float16, device=dev)
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5)
+    close(out, oracle.attention_f64(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5))
+
+
+def test_comfy_backend_strided_layout(dev):
+    """attention_hip on (B, L, H*D) inputs: the kernel reads the strided (B, H, L, D) views and writes (B, L, H, D)."""
+    B, L, H = 1, 640, 3
+    g = gen(8)
+    q, k, v = (torch.randn(B, L, H * 128, generator=g).half() for _ in range(3))
+    out = attention.attention_hip(q.to(dev), k.to(dev), v.to(dev), H)
+    th = lambda t: t.reshape(B, L, H, 128).transpose(1, 2).numpy()  # noqa: E731
+    ref = oracle.attention_f64(th(q), th(k), th(v), 128 ** -0.5)
+    close(out.reshape(B, L, H, 128).transpose(1, 2), ref)
+    out8 = attention.attention_hip_int8(q.to(dev), k.to(dev), v.to(dev), H)
+    close(out8.reshape(B, L, H, 128).transpose(1, 2), oracle.attention_i8qk_f64(th(q), th(k), th(v), 128 ** -0.5))
+
+
+def test_pack_k_i8_bit_exact(dev):
+    B, Hkv, Lk = 1, 2, 100
+    _, k, _ = qkv(B, Hkv, Hkv, 1, Lk, seed=4)
+    lib = _lib.load()
+    ws = torch.empty(lib.rda_attn_i8_workspace(B, Hkv, Lk), dtype=torch.uint8, device=dev)
+    kd = k.to(dev)
+    _lib.check(lib.rda_pack_k_i8(_lib.ptr(kd), _lib.ptr(ws), B, Hkv, Lk, *kd.stride()[:3], _lib.stream()))
+    pad = (Lk + 63) // 64 * 64
+    k8 = ws[:B * Hkv * pad * 128].view(torch.int8).view(B * Hkv, pad, 128).cpu().numpy()
+    ks = ws[B * Hkv * pad * 128:].view(torch.float32).view(B * Hkv, pad).cpu().numpy()
+    for h in range(Hkv):
+        q_ref, s_ref = oracle.quant_rows_rint(k[0, h].numpy())
+        assert np.array_equal(k8[h, :Lk], q_ref)
+        assert np.array_equal(ks[h, :Lk], s_ref)
+        assert not k8[h, Lk:].any()
+
+
+def test_attention_full_size_sampled(dev):
+    """The fused-attention configuration at full size (B=1, H=24, S=4096, D=128): 64 sampled query rows in each of
+    3 sampled heads against the float64 closed form, for fp16 and int8-QK."""
+    B, H, L = 1, 24, 4096
+    q, k, v = qkv(B, H, H, L, L, seed=4)
+    scale = 128 ** -0.5
+    rows = torch.randperm(L, generator=gen(1))[:64].numpy()
+    heads = [0, 11, 23]
+    for int8_qk in (False, True):
+        out = torch.empty(B, H, L, 128, dtype=torch.float16, device=dev)
+        hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, scale, int8_qk)
+        o = out.cpu()
+        for h in heads:
+            qs = q[:, h:h + 1, rows]
+            fn = oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64
+            ref = fn(qs.numpy(), k[:, h:h + 1].numpy(), v[:, h:h + 1].numpy(), scale)
+            close(o[:, h:h + 1, rows], ref)

@@ -1,0 +1,112 @@
+"""Parity of the decode kernels and RMSNorm on the GPU against the oracle.
+
+Bit-exact: the decode rotation (fp32 butterflies, exact power-of-two scale) and RMSNorm (the reference's summation
+order, FMAs, correctly rounded 1/sqrt). Tolerance-based: the GEMVs and decode attention, whose fp32 sums run in a
+different order than any CPU restatement. GEMV bound: |out - ref| <= 1e-5 * scale * sum_k |w x| (+ 2^-10 relative for
+fp16 outputs); decode attention: |out - ref| <= 1e-5 + 1e-4 |ref|."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from comfyui_rdna2_attention_amd import int8_gemv, rms_norm
+from helpers import bits, channel_scales, gen, int8_weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,group", [(1, 256), (3, 1024), (2, 64), (1, 16384), (5, 16)])
+def test_rotate_bit_exact(dev, rows, group):
+    x = torch.randn(rows, group, generator=gen(group)).float()
+    out = int8_gemv.rotate(x.to(dev), group)
+    assert np.array_equal(out.cpu().numpy(), oracle.rotate_f32(x.numpy(), group))
+
+
+def gemv_bound(w, x, scale, half):
+    mag = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64)) * np.abs(scale)
+    return 1e-5 * mag + 1e-12
+
+
+@pytest.mark.parametrize("x_half", [False, True])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536)])
+def test_gemv_i8(dev, N, K, x_half):
+    print(f"gemv_i8 N={N} K={K} half={x_half}", flush=True)
+    x = torch.randn(1, K, generator=gen(16))
+    x = x.half() if x_half else x.float()
+    w = int8_weights(N, K, seed=17)
+    s = channel_scales(N, seed=18)
+    bias = torch.randn(N, generator=gen(19)).float() if N == 64 else None
+    out = int8_gemv.gemv(x.to(dev), w.to(dev), s.to(dev), None if bias is None else bias.to(dev))
+    assert out.dtype == x.dtype and out.shape == (1, N)
+    xf = x.float().numpy().reshape(-1)
+    ref = oracle.gemv_f64(xf, w.numpy(), s.numpy(), None if bias is None else bias.numpy())
+    bound = gemv_bound(w.numpy(), xf, s.numpy(), x_half) + (np.abs(ref) * 2.0 ** -10 if x_half else 0)
+    err = np.abs(out.cpu().double().numpy().reshape(-1) - ref)
+    assert np.all(err <= bound), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("N,K", [(512, 1024), (64, 2560), (8, 256)])
+def test_gemv_bf16(dev, N, K):
+    x = torch.randn(1, 1, K, generator=gen(20)).float()
+    w = torch.randn(N, K, generator=gen(21)).bfloat16()
+    out = int8_gemv.logits_gemv(x.to(dev), w.to(dev))
+    ref = w.double().numpy() @ x.double().numpy().reshape(-1)
+    bound = 1e-5 * (np.abs(w.double().numpy()) @ np.abs(x.double().numpy().reshape(-1)))
+    assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - ref) <= bound)
+
+
+@pytest.mark.parametrize("B,H,Hkv,cap,lengths", [(1, 32, 8, 2048, [2048]), (2, 8, 2, 300, [1, 257]), (1, 4, 4, 64, [33]), (1, 16, 2, 100, [100])])
+def test_attention_decode(dev, B, H, Hkv, cap, lengths):
+    print(f"attention_decode B={B} H={H} Hkv={Hkv} cap={cap} lengths={lengths}", flush=True)
+    g = gen(19)
+    q = torch.randn(B, 1, H, 128, generator=g).float()
+    k = torch.randn(B, cap, Hkv, 128, generator=g).float()
+    v = torch.randn(B, cap, Hkv, 128, generator=g).float()
+    ln = torch.tensor(lengths, dtype=torch.int32)
+    out = int8_gemv.attention_decode(q.to(dev), k.to(dev), v.to(dev), ln.to(dev))
+    ref = oracle.attention_decode_f64(q.numpy(), k.numpy(), v.numpy(), lengths)
+    err = np.abs(out.cpu().double().numpy() - ref)
+    assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 3072), (2, 3, 50, 128), (1, 7, 64), (1, 5, 8192), (2, 9, 136)])
+def test_rms_norm_bit_exact(dev, shape):
+    print(f"rms_norm {shape}", flush=True)
+    g = gen(10)
+    x = torch.randn(*shape, generator=g).half()
+    w = (torch.randn(shape[-1], generator=g) * 0.1).float()  # gain ~ N(1, 0.1), stored zero-centred
+    out = rms_norm.rms_norm(x.to(dev), w.to(dev), 1e-6)
+    assert out.shape == x.shape and out.is_contiguous()
+    assert np.array_equal(bits(out), bits(oracle.rms_norm(x.numpy(), w.numpy(), 1e-6)))
+
+
+def test_rms_norm_strided_heads(dev):
+    """(B, H, L, D) views of a (B, L, H*D) buffer: the kernel reads with strides, writes contiguous (B, H, L, D)."""
+    B, L, H, D = 2, 33, 4, 128
+    g = gen(11)
+    base = torch.randn(B, L, H * D, generator=g).half()
+    w = (torch.randn(D, generator=g) * 0.1).float()
+    view = base.to(dev).view(B, L, H, D).transpose(1, 2)
+    out = rms_norm.rms_norm(view, w.to(dev), 1e-6)
+    ref = oracle.rms_norm(base.view(B, L, H, D).transpose(1, 2).contiguous().numpy(), w.numpy(), 1e-6)
+    assert np.array_equal(bits(out), bits(ref))
+
+
+class _Norm:
+    def __init__(self, scale, eps):
+        self.scale, self.eps = scale, eps
+
+
+@pytest.mark.parametrize("fb", [1, 2])
+def test_rms_norm_rope_bit_exact(dev, fb):
+    B, L, H = 2, 40, 3
+    g = gen(12)
+    x = torch.randn(B, L, H * 128, generator=g).half()
+    w = (torch.randn(128, generator=g) * 0.1).float()
+    ang = torch.randn(fb, 1, L, 64, generator=g)
+    freqs = torch.stack([torch.cos(ang), -torch.sin(ang), torch.sin(ang), torch.cos(ang)], -1).reshape(fb, 1, L, 64, 2, 2).float()
+    out = rms_norm.rms_norm_rope(x.to(dev), H, _Norm(w.to(dev), 1e-6), freqs.to(dev))
+    xh = x.view(B, L, H, 128).transpose(1, 2).contiguous().numpy()
+    f = freqs.numpy() if fb > 1 else np.broadcast_to(freqs.numpy(), (B,) + freqs.shape[1:])
+    ref = oracle.rms_norm(xh, w.numpy(), 1e-6, freqs=np.ascontiguousarray(f))
+    assert np.array_equal(bits(out), bits(ref))

@@ -1,0 +1,195 @@
+"""Parity of the linear path on the GPU (through the C ABI) against the oracle: quantized activations and scales
+bit-exact, int32 accumulators bit-exact, fp16 outputs bit-exact (the epilogue is IEEE fp32 in a fixed order)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from comfyui_rdna2_attention_amd import int8_gemm
+from helpers import activations, bits, channel_scales, gen, int4_weights, int8_weights, q_of
+
+pytestmark = pytest.mark.gpu
+
+
+def kern():
+    return int8_gemm.get_kernels()
+
+
+@pytest.mark.parametrize("M,K,group", [(7, 256, 256), (300, 3072, 256), (257, 3072, 128), (64, 16384, 256), (33, 8192, 128), (5, 128, 128)])
+def test_rot_quant_bit_exact(dev, M, K, group):
+    print(f"rot_quant M={M} K={K} group={group}", flush=True)
+    x = activations(M, K, seed=M + K)
+    x[M // 2] = 0  # an all-zero row: scale 1e-30, codes 0
+    packed, scale = int8_gemm.quantize(kern().rot_quant_pack_a, x.to(dev), K, group=group)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), group=group)
+    assert np.array_equal(scale.cpu().numpy(), s_ref)
+    assert np.array_equal(q_of(packed, M, K), q_ref)
+
+
+@pytest.mark.parametrize("M,K", [(3, 64), (100, 3072), (9, 16384)])
+def test_quant_pack_a_bit_exact(dev, M, K):
+    print(f"quant_pack_a M={M} K={K}", flush=True)
+    x = activations(M, K, seed=3)
+    packed, scale = int8_gemm.quantize(kern().quant_pack_a, x.to(dev), K)
+    q_ref, s_ref = oracle.quant_rows(x.numpy())
+    assert np.array_equal(scale.cpu().numpy(), s_ref)
+    assert np.array_equal(q_of(packed, M, K), q_ref)
+
+
+@pytest.mark.parametrize("act", ["swiglu", "gate", "situ"])
+@pytest.mark.parametrize("M,K,group", [(37, 1024, 256), (16, 8192, 256), (21, 512, 128)])
+def test_activation_rot_quant_bit_exact(dev, act, M, K, group):
+    print(f"{act}_rot_quant M={M} K={K} group={group}", flush=True)
+    g = gen(11)
+    k = kern()
+    if act == "situ":
+        x = (torch.randn(M, 2 * K, generator=g) * 3).half()
+        packed, scale = int8_gemm.quantize(k.situ_rot_quant_pack_a, x.to(dev), K, group=group)
+        q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), act=oracle.ACT_SITU, group=group)
+    else:
+        a = (torch.randn(M, K, generator=g) * 4).half()
+        b = (torch.randn(M, K, generator=g) * 4).half()
+        entry = k.swiglu_rot_quant_pack_a if act == "swiglu" else k.gate_rot_quant_pack_a
+        packed, scale = int8_gemm.quantize(entry, a.to(dev), K, up=b.to(dev), group=group)
+        q_ref, s_ref, _ = oracle.rot_quant_rows(a.numpy(), act=oracle.ACT_SWIGLU if act == "swiglu" else oracle.ACT_GATE, group=group, u=b.numpy())
+    assert np.array_equal(scale.cpu().numpy(), s_ref)
+    assert np.array_equal(q_of(packed, M, K), q_ref)
+
+
+@pytest.mark.parametrize("B,L,K", [(1, 77, 3072), (2, 40, 1024)])
+def test_mod_rot_quant_bit_exact(dev, B, L, K):
+    print(f"mod_rot_quant B={B} L={L} K={K}", flush=True)
+    g = gen(5)
+    x = torch.randn(B * L, K, generator=g).half()
+    w = (torch.randn(K, generator=g) * 0.1).float()
+    s = (1 + torch.randn(B, K, generator=g) * 0.2).half()
+    t = (torch.randn(B, K, generator=g) * 0.2).half()
+    eps = 1e-6
+    packed, scale = int8_gemm.quantized(B * L, K, dev)
+    p = int8_gemm._lib.ptr
+    int8_gemm.launch(kern().mod_rot_quant_pack_a, 0, 0, 0, [p(x.to(dev)), p(packed), p(scale), B * L, K, p(w.to(dev)), p(s.to(dev)), p(t.to(dev)), L, eps])
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), act=oracle.ACT_MOD, mod=(w.numpy(), s.numpy(), t.numpy(), L, eps))
+    assert np.array_equal(scale.cpu().numpy(), s_ref)
+    assert np.array_equal(q_of(packed, B * L, K), q_ref)
+
+
+@pytest.mark.parametrize("M,K", [(40, 1024), (9, 3072)])
+def test_rot_quant_i4_bit_exact(dev, M, K):
+    x = activations(M, K, seed=17)
+    packed, scale = int8_gemm.quantize(kern().rot_quant_pack_a_i4, x.to(dev), K)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), i4=True)
+    assert np.array_equal(scale.cpu().numpy(), s_ref)
+    q = q_of(packed, M, K)
+    assert np.abs(q).max() <= 7
+    assert np.array_equal(q, q_ref)
+
+
+def packed_from(a_int8):
+    return torch.from_numpy(np.ascontiguousarray(a_int8)).view(torch.int32).reshape(-1)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 3072), (1000, 192, 512), (513, 64, 64), (256, 256, 8192), (77, 128, 1024), (300, 320, 192)])
+def test_gemm_int32_accumulators_exact(dev, M, N, K):
+    print(f"gemm_acc M={M} N={N} K={K}", flush=True)
+    g = gen(M + N + K)
+    a = torch.randint(-128, 128, (M, K), generator=g, dtype=torch.int8).numpy()
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    acc = int8_gemm.gemm_acc(packed_from(a).to(dev), w.to(dev), M, K)
+    assert np.array_equal(acc.cpu().numpy(), oracle.gemm_acc(a, w.numpy()))
+
+
+@pytest.mark.parametrize("M,N,K", [(600, 256, 1024), (128, 64, 256), (1000, 384, 512)])
+def test_gemm_int4_weight_accumulators_exact(dev, M, N, K):
+    print(f"gemm_acc int4 M={M} N={N} K={K}", flush=True)
+    a = torch.randint(-128, 128, (M, K), generator=gen(1), dtype=torch.int8).numpy()
+    w, wp = int4_weights(N, K, seed=2)
+    acc = int8_gemm.gemm_acc(packed_from(a).to(dev), wp.to(dev), M, K, int4=True)
+    assert np.array_equal(oracle.unpack_int4(wp.numpy(), K), w.numpy())
+    assert np.array_equal(acc.cpu().numpy(), oracle.gemm_acc(a, w.numpy()))
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("M,N,K,group", [(4096, 3072, 3072, 128), (520, 256, 1024, 256), (700, 192, 768, 256), (515, 64, 512, 128)])
+def test_w8a8_linear_bit_exact(dev, M, N, K, group, bias):
+    print(f"w8a8 linear M={M} N={N} K={K} group={group} bias={bias}", flush=True)
+    x = activations(M, K, seed=1)
+    w = int8_weights(N, K, seed=2)
+    ws = channel_scales(N, seed=3)
+    b = (torch.randn(N, generator=gen(4)) * 0.5).half() if bias else None
+    out = int8_gemm.linear(x.to(dev), w.to(dev), ws.to(dev), None if b is None else b.to(dev), rotate=True, group=group)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), group=group)
+    ref = oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy(), None if b is None else b.numpy())
+    assert np.array_equal(bits(out), bits(ref))
+
+
+def test_gemm_residual_epilogue_bit_exact(dev):
+    B, L, K, N = 2, 300, 512, 256
+    M = B * L
+    g = gen(9)
+    x = activations(M, K, seed=7)
+    w = int8_weights(N, K, seed=8)
+    ws = channel_scales(N, seed=9)
+    R = torch.randn(M, N, generator=g).half()
+    G = torch.randn(B, N, generator=g).half()
+    out = int8_gemm.linear(x.to(dev), w.to(dev), ws.to(dev), None, rotate=True, res=(R.to(dev), G.to(dev)))
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    ref = oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy(), R=R.numpy(), G=G.numpy(), L=L)
+    assert np.array_equal(bits(out), bits(ref))
+
+
+def test_swiglu_down_linear_bit_exact(dev):
+    M, K, N = 512, 2048, 256
+    g = gen(12)
+    gate = torch.randn(M, K, generator=g).half()
+    up = torch.randn(M, K, generator=g).half()
+    w = int8_weights(N, K, seed=13)
+    ws = channel_scales(N, seed=14)
+    out = int8_gemm.linear(gate.to(dev), w.to(dev), ws.to(dev), None, up=up.to(dev))
+    q_ref, s_ref, _ = oracle.rot_quant_rows(gate.numpy(), act=oracle.ACT_SWIGLU, u=up.numpy())
+    ref = oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())
+    assert np.array_equal(bits(out), bits(ref))
+
+
+@pytest.mark.parametrize("M,N,K", [(520, 512, 1024), (300, 192, 384), (4096, 1024, 3072)])
+def test_w4a8_bit_exact(dev, M, N, K):
+    print(f"w4a8 M={M} N={N} K={K}", flush=True)
+    x = activations(M, K, seed=7, outliers=0)
+    w, wp = int4_weights(N, K, seed=8)
+    gs = (torch.rand(N, K // 128, generator=gen(9)) * 1.5e-2 + 5e-3).half()
+    out = int8_gemm.linear_w4a8(x.to(dev), wp.to(dev), gs.to(dev))
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    ref = oracle.w4a8_epilogue(oracle.w4a8_partials(q_ref, w.numpy()), s_ref, gs.numpy())
+    assert np.array_equal(bits(out), bits(ref))
+
+
+def test_w4a8_full_size_sampled_rows(dev):
+    """The W4A8 configuration at full size (4096 x 12288 x 3072): every output row of a seeded sample of 48 rows
+    against the oracle, bit for bit."""
+    M, N, K = 4096, 12288, 3072
+    x = activations(M, K, seed=7, outliers=0)
+    w, wp = int4_weights(N, K, seed=8)
+    gs = (torch.rand(N, K // 128, generator=gen(9)) * 1.5e-2 + 5e-3).half()
+    out = int8_gemm.linear_w4a8(x.to(dev), wp.to(dev), gs.to(dev)).cpu().numpy()
+    rows = torch.randperm(M, generator=gen(10))[:48].numpy()
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy()[rows])
+    ref = oracle.w4a8_epilogue(oracle.w4a8_partials(q_ref, w.numpy()), s_ref, gs.numpy())
+    assert np.array_equal(bits(out[rows]), bits(ref))
+
+
+def test_w4a4_hook_path_bit_exact(dev):
+    """rot_quant_pack_a_i4 + gemm_i4 (the convrot_w4a4_forward replacement) against the oracle."""
+    M, N, K = 600, 256, 1024
+    x = activations(M, K, seed=21)
+    w, wp = int4_weights(N, K, seed=22)
+    ws = channel_scales(N, seed=23)
+    k = kern()
+    out = int8_gemm.run(k.rot_quant_pack_a_i4, k.gemm_i4, x.to(dev), wp.to(dev), ws.to(dev), None, K)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), i4=True)
+    ref = oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())
+    assert np.array_equal(bits(out), bits(ref))
+
+
+def test_rejects_unsupported_shapes(dev):
+    x = activations(8, 100, seed=1)
+    with pytest.raises(RuntimeError, match="HIP error 1"):
+        int8_gemm.quantize(kern().rot_quant_pack_a, x.to(dev), 100)

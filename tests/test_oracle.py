@@ -1,0 +1,280 @@
+"""Pins the CPU oracle independently of its own formulas: closed forms (the Hadamard matrix, exact integer
+products), library routines (numpy's fp16 conversion, math.exp), invariants of the quantizer, float64 references
+and brute force on tiny inputs. The reference ships no golden vectors or tests for this path, so these checks
+are what fix the oracle; tests/golden/ then freezes it."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import ACT_GATE, ACT_MOD, ACT_SITU, ACT_SWIGLU
+
+rng = np.random.default_rng(1234)
+
+
+def test_fp16_conversions_match_numpy():
+    L = oracle.lib()
+    h = np.arange(65536, dtype=np.uint16)
+    f = np.array([L.orc_h2f(int(v)) for v in h], dtype=np.float32)
+    ref = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(f[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.all(np.isnan(f[np.isnan(ref)]))
+    # f2h on random floats over the whole fp16 range, plus halfway cases, subnormals and overflow.
+    xs = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 20000),
+                         (np.arange(0, 2048, dtype=np.float32) + 0.5) * 2.0 ** -24,  # halfway between subnormals
+                         np.float32([65504, 65519.9, 65520, 1e9, -1e9, 0.0, -0.0, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8])]).astype(np.float32)
+    got = np.array([L.orc_f2h(float(x)) for x in xs], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(got, xs.astype(np.float16).view(np.uint16))
+
+
+def ulp32(v):
+    return float(np.spacing(np.float32(abs(v))))
+
+
+def ulp_err(got, x):
+    ref = math.exp(x)
+    return abs(float(got) - ref) / ulp32(ref)
+
+
+def test_exp_accuracy():
+    xs = np.concatenate([np.linspace(-88, 88.7, 20001), rng.uniform(-20, 20, 5000)]).astype(np.float32)
+    worst = max(ulp_err(oracle.expf(x), float(x)) for x in xs)
+    assert worst <= 2.0, worst
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(-100.0) == 0.0 and math.isinf(oracle.expf(100.0))
+
+
+def test_exp2_accuracy():
+    ys = np.concatenate([np.linspace(-126, 127.9, 20001), rng.uniform(-10, 10, 5000)]).astype(np.float32)
+    worst = max(abs(float(oracle.exp2f(y)) - 2.0 ** float(y)) / ulp32(2.0 ** float(y)) for y in ys)
+    assert worst <= 2.0, worst
+    for n in range(-126, 128):
+        assert oracle.exp2f(float(n)) == 2.0 ** n  # exact on integers
+
+
+@pytest.mark.parametrize("group", [256, 128])
+def test_hadamard_closed_form(group):
+    H = oracle.hadamard_matrix(group)
+    assert np.array_equal(H @ H.T, group * np.eye(group, dtype=np.int64))
+    if group == 256:
+        assert np.array_equal(H, H.T)
+        assert np.all(H.sum(1) == 16)  # regular: every row sums to sqrt(256)
+    # Integer inputs small enough that every fp32 butterfly is exact: the oracle's rotation must equal H x scaled
+    # (scale 1/16 exact for 256; for 128 compare before the inexact 2^-3.5 via the fp16-rounded output bound).
+    x = rng.integers(-8, 9, (3, group)).astype(np.float16)
+    _, _, rot = oracle.rot_quant_rows(x, group=group)
+    exact = (x.astype(np.float64) @ H.T) * (1 / 16 if group == 256 else 2 ** -3.5)
+    if group == 256:
+        assert np.array_equal(rot, exact.astype(np.float16))
+    else:
+        assert np.all(np.abs(rot.astype(np.float64) - exact) <= np.abs(exact) * 2 ** -11 + 1e-7)
+
+
+def test_rotation_of_random_rows_close_to_closed_form():
+    x = (rng.standard_normal((5, 1024)) * 3).astype(np.float16)
+    for group in (256, 128):
+        _, _, rot = oracle.rot_quant_rows(x, group=group)
+        H = oracle.hadamard_matrix(group) / math.sqrt(group)
+        exact = (x.astype(np.float64).reshape(5, -1, group) @ H.T).reshape(5, -1)
+        assert np.all(np.abs(rot.astype(np.float64) - exact) <= np.abs(exact) * 2 ** -10 + 1e-3)
+
+
+def test_rotation_stage_order_pinned():
+    """The digit order (1, 4, 16, 64) matters in fp32; a restatement in another order must differ on some input."""
+    x = (rng.standard_normal((64, 256)) * 1000).astype(np.float16)
+    _, _, rot = oracle.rot_quant_rows(x)
+    H4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], np.float32)
+    v = x.astype(np.float32).reshape(64, 4, 4, 4, 4)  # axes: d3 d2 d1 d0
+    for axis in (1, 2, 3, 4):  # reversed digit order: 64, 16, 4, 1
+        v = np.moveaxis(np.tensordot(v, H4, axes=([axis], [1])).astype(np.float32), -1, axis)
+    other = (v.reshape(64, 256) * np.float32(0.0625)).astype(np.float16)
+    assert not np.array_equal(other, rot)
+    assert np.all(np.abs(other.astype(np.float32) - rot.astype(np.float32)) <= np.abs(rot.astype(np.float32)) * 2 ** -9 + 1e-2)
+
+
+def quant_invariants(q, s, rot, qmax):
+    r = rot.astype(np.float32)
+    mx = np.abs(r).max(1)
+    nonzero = mx > 0
+    assert np.all(np.abs(q).max(1)[nonzero] == qmax)
+    assert np.all(q[~nonzero] == 0)
+    # |x - q s| <= s / 2 (plus the rounding of x / s) wherever the code is not clamped
+    err = np.abs(r - q.astype(np.float32) * s[:, None])
+    assert np.all(err <= s[:, None] * (0.5 + 1e-5))
+
+
+def test_quantizer_invariants():
+    x = (rng.standard_normal((20, 2048)) * rng.uniform(0.01, 100, (20, 1))).astype(np.float16)
+    x[3] = 0
+    q, s, rot = oracle.rot_quant_rows(x)
+    assert s[3] == np.float32(1e-30)
+    assert np.array_equal(s, np.maximum(np.abs(rot.astype(np.float32)).max(1) / np.float32(127), np.float32(1e-30)))
+    quant_invariants(q, s, rot, 127)
+    q4, s4, rot4 = oracle.rot_quant_rows(x, i4=True)
+    assert np.array_equal(rot4, rot)
+    assert np.all(np.abs(q4) <= 7)
+    quant_invariants(q4[np.arange(20) != 3], s4[np.arange(20) != 3], rot[np.arange(20) != 3], 7)
+
+
+def test_quant_rounding_brute_force():
+    """floor(x / s + 0.5) versus exact rational rounding on values engineered at and near .5 boundaries."""
+    from fractions import Fraction
+    x = np.zeros((1, 256), np.float16)
+    x[0, 0] = 127.0
+    x[0, 1:127] = (np.arange(126) + 0.5).astype(np.float16)  # exact halves: 0.5 .. 125.5
+    x[0, 127:253] = -(np.arange(126) + 0.5).astype(np.float16)
+    q, s = oracle.quant_rows(x)
+    assert s[0] == np.float32(1.0)
+    for v, code in zip(x[0].astype(np.float32), q[0]):
+        assert code == max(-128, min(127, math.floor(Fraction(float(v)) + Fraction(1, 2))))
+
+
+def test_activations_close_to_float64():
+    g = (rng.standard_normal(3000) * 6).astype(np.float16).astype(np.float32)
+    u = (rng.standard_normal(3000) * 3).astype(np.float16).astype(np.float32)
+    sw = oracle.vectorize("orc_swiglu", g, u)
+    silu = g / (1 + np.exp(-g.astype(np.float64)))
+    ref = silu.astype(np.float16).astype(np.float64) * u
+    assert np.all(np.abs(sw - ref) <= np.abs(ref) * 2 ** -10 + np.abs(u) * 2 ** -10 * np.abs(silu) + 1e-6)
+    sg = oracle.vectorize("orc_sigmoid_gate", u, g)
+    ref = u * (1 / (1 + np.exp(-g.astype(np.float64))))
+    assert np.all(np.abs(sg - ref) <= np.abs(ref) * 2 ** -9 + 1e-6)
+    st = oracle.vectorize("orc_situ", u, g)
+    tanh = np.tanh
+    ref = 4 * tanh(g / 4) / (1 + np.exp(-g.astype(np.float64))) * 25 * tanh(u * 0.04)
+    assert np.all(np.abs(st - ref) <= np.abs(ref) * 2 ** -9 + 1e-5)
+
+
+def test_mod_quant_equals_norm_modulate_then_rotate():
+    """ACT_MOD = RMSNorm (rms_norm_row order) -> modulate -> rotate: the same codes as composing the oracle's
+    rms_norm with a float64-checked modulation and the plain rotate-quant."""
+    B, L, K = 2, 5, 768
+    x = rng.standard_normal((B * L, K)).astype(np.float16)
+    w = (rng.standard_normal(K) * 0.1).astype(np.float32)
+    s = (1 + rng.standard_normal((B, K)) * 0.2).astype(np.float16)
+    t = (rng.standard_normal((B, K)) * 0.2).astype(np.float16)
+    q, sc, _ = oracle.rot_quant_rows(x, act=ACT_MOD, mod=(w, s, t, L, 1e-6))
+    normed = oracle.rms_norm(x[None], w, 1e-6)[0]  # fp16(x * rstd * (w + 1)), the rms_norm_row order
+    srow = np.repeat(s, L, axis=0).astype(np.float32)
+    trow = np.repeat(t, L, axis=0).astype(np.float32)
+    mod = ((normed.astype(np.float32) * srow).astype(np.float16).astype(np.float32) + trow).astype(np.float16)
+    q2, sc2, _ = oracle.rot_quant_rows(mod)
+    assert np.array_equal(q, q2) and np.array_equal(sc, sc2)
+
+
+def test_gemm_acc_brute_force():
+    a = rng.integers(-128, 128, (5, 96)).astype(np.int8)
+    w = rng.integers(-128, 128, (7, 96)).astype(np.int8)
+    brute = np.array([[sum(int(a[m, k]) * int(w[n, k]) for k in range(96)) for n in range(7)] for m in range(5)])
+    assert np.array_equal(oracle.gemm_acc(a, w), brute)
+
+
+def test_gemm_epilogue_close_to_float64():
+    acc = rng.integers(-2 ** 22, 2 ** 22, (16, 64)).astype(np.int32)
+    a_s = rng.uniform(1e-3, 1, 16).astype(np.float32)
+    w_s = rng.uniform(1e-3, 3e-3, 64).astype(np.float32)
+    bias = rng.standard_normal(64).astype(np.float16)
+    out = oracle.gemm_epilogue(acc, a_s, w_s, bias)
+    ref = acc.astype(np.float64) * a_s[:, None] * w_s[None] + bias.astype(np.float64)
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= np.abs(ref) * 2 ** -10 + 1e-6)
+    R = rng.standard_normal((16, 64)).astype(np.float16)
+    G = rng.standard_normal((2, 64)).astype(np.float16)
+    y = oracle.gemm_epilogue(acc, a_s, w_s)
+    out = oracle.gemm_epilogue(acc, a_s, w_s, R=R, G=G, L=8)
+    ref = R.astype(np.float64) + np.repeat(G, 8, 0).astype(np.float64) * y.astype(np.float64)
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= np.abs(ref) * 2 ** -9 + 2 ** -14)
+
+
+def test_w4a8_epilogue_close_to_float64():
+    parts = rng.integers(-2 ** 16, 2 ** 16, (6, 8, 32)).astype(np.int32)
+    a_s = rng.uniform(1e-3, 1, 8).astype(np.float32)
+    gs = rng.uniform(5e-3, 2e-2, (32, 6)).astype(np.float16)
+    out = oracle.w4a8_epilogue(parts, a_s, gs)
+    ref = np.einsum("gmn,ng->mn", parts.astype(np.float64), gs.astype(np.float64)) * a_s[:, None]
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= np.abs(ref) * 2 ** -10 + 1e-4)
+
+
+def test_int4_pack_round_trip():
+    w = rng.integers(-8, 8, (9, 64)).astype(np.int8)
+    p = oracle.pack_int4(w)
+    assert p.shape == (9, 32)
+    assert (p[0, 0] & 0xF) == (int(w[0, 0]) & 0xF)  # low nibble holds the even k
+    assert np.array_equal(oracle.unpack_int4(p, 64), w)
+
+
+@pytest.mark.parametrize("D", [64, 128, 3072])
+def test_rms_norm_close_to_float64(D):
+    x = rng.standard_normal((2, 3, D)).astype(np.float16)
+    w = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    out = oracle.rms_norm(x, w, 1e-6)
+    ref = oracle.rms_norm_f64(x, w, 1e-6)
+    assert np.all(np.abs(out.astype(np.float64) - ref) <= np.abs(ref) * 2 ** -10 + 2 ** -24)
+
+
+def test_rms_norm_summation_is_the_reference_tree():
+    """For TPR 256 the sum of squares must follow the thread/butterfly tree; a sequential fp32 sum differs on some
+    rows, and both stay within the fp32 error bound of the exact sum."""
+    D = 8192
+    x = (rng.standard_normal((64, D)) * rng.uniform(0.1, 50, (64, 1))).astype(np.float16)
+    w = np.zeros(D, np.float32)
+    out = oracle.rms_norm(x[None], w, 0.0)[0].astype(np.float32)
+    seq = np.array([np.float32(0)] * 64)
+    xf = x.astype(np.float32)
+    for m in range(64):
+        s = np.float32(0)
+        for v in xf[m]:
+            s = np.float32(s + v * v)
+        seq[m] = s
+    seq_out = (xf * (np.float32(1) / np.sqrt(seq / np.float32(D)))[:, None]).astype(np.float16).astype(np.float32)
+    assert not np.array_equal(out, seq_out)
+    ref = oracle.rms_norm_f64(x, w, 0.0)
+    assert np.all(np.abs(out - ref) <= np.abs(ref) * 2 ** -10 + 2 ** -24)
+
+
+def test_rotate_f32_closed_form():
+    x = rng.integers(-8, 9, (2, 256)).astype(np.float32)
+    out = oracle.rotate_f32(x, 256)
+    assert np.array_equal(out, (x.astype(np.float64) @ oracle.hadamard_matrix(256).T / 16).astype(np.float32))
+
+
+def test_attention_restatements_agree():
+    q = rng.standard_normal((1, 2, 40, 128)).astype(np.float16)
+    k = rng.standard_normal((1, 1, 70, 128)).astype(np.float16)
+    v = rng.standard_normal((1, 1, 70, 128)).astype(np.float16)
+    ref = oracle.attention_f64(q, k, v, 128 ** -0.5)
+    faithful = oracle.attention_faithful(q, k, v, 128 ** -0.5)
+    assert np.abs(faithful.astype(np.float64) - ref).max() < 1e-3
+    i8 = oracle.attention_i8qk_f64(q, k, v, 128 ** -0.5)
+    assert np.abs(i8 - ref).max() < 2e-2  # int8 scores: ~1% perturbation of the logits
+    # brute-force softmax for one row
+    s = [sum(float(q[0, 1, 3, d]) * float(k[0, 0, j, d]) for d in range(128)) / math.sqrt(128) for j in range(70)]
+    p = [math.exp(x - max(s)) for x in s]
+    row = [sum(p[j] * float(v[0, 0, j, d]) for j in range(70)) / sum(p) for d in range(128)]
+    assert np.allclose(ref[0, 1, 3], row, atol=1e-12)
+
+
+def test_decode_attention_closed_form():
+    q = rng.standard_normal((1, 1, 8, 128)).astype(np.float32)
+    k = rng.standard_normal((1, 50, 2, 128)).astype(np.float32)
+    v = rng.standard_normal((1, 50, 2, 128)).astype(np.float32)
+    out = oracle.attention_decode_f64(q, k, v, [37])
+    ref = oracle.attention_f64(q.transpose(0, 2, 1, 3), k[:, :37].transpose(0, 2, 1, 3), v[:, :37].transpose(0, 2, 1, 3), 128 ** -0.5)
+    assert np.allclose(out[0, 0], ref[0, :, 0], atol=1e-12)
+
+
+@pytest.mark.parametrize("act", [ACT_SWIGLU, ACT_GATE, ACT_SITU])
+def test_activation_paths_rotate_the_activation(act):
+    """Activation -> rotate-quant equals applying the scalar activation first and then the plain rotate-quant."""
+    M, K = 3, 512
+    a = (rng.standard_normal((M, 2 * K if act == ACT_SITU else K)) * 3).astype(np.float16)
+    b = (rng.standard_normal((M, K)) * 3).astype(np.float16)
+    q, s, _ = oracle.rot_quant_rows(a, act=act, u=None if act == ACT_SITU else b)
+    if act == ACT_SITU:
+        pre = oracle.vectorize("orc_situ", a[:, :K], a[:, K:])
+    else:
+        pre = oracle.vectorize("orc_swiglu" if act == ACT_SWIGLU else "orc_sigmoid_gate", a, b)
+    q2, s2, _ = oracle.rot_quant_rows(pre.astype(np.float16))
+    assert np.array_equal(q, q2) and np.array_equal(s, s2)
