@@ -255,8 +255,8 @@ __global__ __launch_bounds__(AT, 2) void attn_kernel(AttnArgs p) {
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++) {
-                const h4v w = {(half_t)(o[dt][r4 * 4] * inv), (half_t)(o[dt][r4 * 4 + 1] * inv), (half_t)(o[dt][r4 * 4 + 2] * inv),
-                               (half_t)(o[dt][r4 * 4 + 3] * inv)};
+                const h4v w = {to_half(o[dt][r4 * 4] * inv), to_half(o[dt][r4 * 4 + 1] * inv), to_half(o[dt][r4 * 4 + 2] * inv),
+                               to_half(o[dt][r4 * 4 + 3] * inv)};
                 *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
             }
     }

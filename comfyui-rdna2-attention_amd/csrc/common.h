@@ -23,8 +23,15 @@ typedef u32 u4v __attribute__((ext_vector_type(4)));
 
 #define RDA_ERR_INVALID 1  // hipErrorInvalidValue
 
-// Rounds an fp32 value to fp16 and back (one RNE rounding).
-__device__ __forceinline__ float r16(float x) { return (float)(half_t)x; }
+// fp32 -> fp16 (RNE) of a value that has been rounded to fp32 first. Without the register barrier the compiler
+// folds a preceding fp32 multiply or FMA into v_fma_mixlo_f16, which rounds the exact product once, straight to
+// fp16; every rounding point in these kernels is "round to fp32, then to fp16", as the arithmetic is written.
+__device__ __forceinline__ half_t to_half(float x) {
+    asm volatile("" : "+v"(x));
+    return (half_t)x;
+}
+// Rounds an fp32 value to fp16 and back.
+__device__ __forceinline__ float r16(float x) { return (float)to_half(x); }
 
 // exp(x): 2^n e^r with n = rint(x log2 e), r = x - n ln2 by a two-constant
 // Cody-Waite reduction, e^r by a degree-7 Taylor polynomial in Horner form, and

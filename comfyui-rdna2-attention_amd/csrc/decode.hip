@@ -94,7 +94,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const void* __re
         float sum = wave_sum(acc[r]) * scale[row + r];
         if (bias) sum = sum + bias[row + r];
         if (lane == 0) {
-            if (XH) ((half_t*)out)[row + r] = (half_t)sum;
+            if (XH) ((half_t*)out)[row + r] = to_half(sum);
             else ((float*)out)[row + r] = sum;
         }
     }

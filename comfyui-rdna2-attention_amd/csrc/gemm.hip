@@ -207,7 +207,7 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const int8_t* __restrict__ 
                     if (bias) y = y + (float)bv[j];
                 }
                 const int rr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                *(half_t*)(stage + rr * SP + (j * 32 + (lane & 31)) * 2) = (half_t)y;
+                *(half_t*)(stage + rr * SP + (j * 32 + (lane & 31)) * 2) = to_half(y);
             }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const int8_t* __restrict__ 
                 if (R) {
                     const h8 res = *(const h8*)(R + at), gate = *(const h8*)(G + (size_t)(m / L) * N + n);
 #pragma unroll
-                    for (int e = 0; e < 8; e++) y[e] = (half_t)((float)res[e] + r16((float)gate[e] * (float)y[e]));
+                    for (int e = 0; e < 8; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
                 }
                 *(h8*)(C + at) = y;
             }

@@ -50,20 +50,18 @@ __global__ __launch_bounds__(NT) void norm_kernel(const half_t* __restrict__ X, 
             const f4 lo = ((const f4*)W)[i * 2], hi = ((const f4*)W)[i * 2 + 1];
             h8 o;
 #pragma unroll
-            for (int j = 0; j < 8; j++) o[j] = (half_t)((float)v[c][j] * rstd * ((j < 4 ? lo[j & 3] : hi[j & 3]) + 1.f));
+            for (int j = 0; j < 8; j++) o[j] = to_half((float)v[c][j] * rstd * ((j < 4 ? lo[j & 3] : hi[j & 3]) + 1.f));
             if (ROPE) {
-                // rms_norm.hip:48-61: a = fma(m1, x1, fp32(m0 x0)), c = fma(m3, x1, fp32(m2 x0)). The fp32
-                // result is pinned in a register before the fp16 conversion, so it is rounded twice
-                // (to fp32, then fp16) like the reference, never straight to fp16.
+                // rms_norm.hip:48-61: a = fma(m1, x1, fp32(m0 x0)), c = fma(m3, x1, fp32(m2 x0)), each
+                // rounded to fp32 and then to fp16 (to_half), like the reference.
                 const f4* f = F + b * fb + (long)l * (D / 2) + i * 4;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const f4 m = f[j];
                     const float x0 = (float)o[j * 2], x1 = (float)o[j * 2 + 1];
-                    float a = __builtin_fmaf(m[1], x1, m[0] * x0), cc = __builtin_fmaf(m[3], x1, m[2] * x0);
-                    asm volatile("" : "+v"(a), "+v"(cc));
-                    o[j * 2] = (half_t)a;
-                    o[j * 2 + 1] = (half_t)cc;
+                    const float a = __builtin_fmaf(m[1], x1, m[0] * x0), cc = __builtin_fmaf(m[3], x1, m[2] * x0);
+                    o[j * 2] = to_half(a);
+                    o[j * 2 + 1] = to_half(cc);
                 }
             }
             y[i] = o;

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
                 }
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const half_t y = (half_t)(v[i] * norm);
+                    const half_t y = to_half(v[i] * norm);
                     rotated[g * GROUP + e[i]] = y;
                     mx = fmaxf(mx, fabsf((float)y));
                 }

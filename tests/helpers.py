@@ -42,3 +42,15 @@ def q_of(packed, M, K):
 def bits(t):
     a = t.detach().cpu().numpy() if isinstance(t, torch.Tensor) else np.asarray(t)
     return np.ascontiguousarray(a, dtype=np.float16).view(np.uint16)
+
+
+def assert_same(got, ref, what=""):
+    """Bit-exact comparison that reports how many elements differ and where."""
+    got, ref = np.asarray(got), np.asarray(ref)
+    assert got.shape == ref.shape, f"{what} shape {got.shape} != {ref.shape}"
+    if got.dtype.kind == "f":
+        got, ref = got.view(np.uint8 if got.itemsize == 1 else f"u{got.itemsize}"), ref.astype(got.dtype).view(f"u{got.itemsize}")
+    bad = np.argwhere(got != ref)
+    if len(bad):
+        where = ", ".join(f"{tuple(int(v) for v in i)}: {got[tuple(i)]} vs {ref[tuple(i)]}" for i in bad[:5])
+        raise AssertionError(f"{what} {len(bad)} of {got.size} elements differ; first: {where}")

@@ -11,7 +11,7 @@ import torch
 
 import oracle
 from comfyui_rdna2_attention_amd import _lib, attention, hip_attention
-from helpers import gen
+from helpers import assert_same, gen
 
 pytestmark = pytest.mark.gpu
 
@@ -89,8 +89,8 @@ def test_pack_k_i8_bit_exact(dev):
     ks = ws[B * Hkv * pad * 128:].view(torch.float32).view(B * Hkv, pad).cpu().numpy()
     for h in range(Hkv):
         q_ref, s_ref = oracle.quant_rows_rint(k[0, h].numpy())
-        assert np.array_equal(k8[h, :Lk], q_ref)
-        assert np.array_equal(ks[h, :Lk], s_ref)
+        assert_same(k8[h, :Lk], q_ref)
+        assert_same(ks[h, :Lk], s_ref)
         assert not k8[h, Lk:].any()
 
 

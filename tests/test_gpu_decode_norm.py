@@ -10,7 +10,7 @@ import torch
 
 import oracle
 from comfyui_rdna2_attention_amd import int8_gemv, rms_norm
-from helpers import bits, channel_scales, gen, int8_weights
+from helpers import assert_same, bits, channel_scales, gen, int8_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 def test_rotate_bit_exact(dev, rows, group):
     x = torch.randn(rows, group, generator=gen(group)).float()
     out = int8_gemv.rotate(x.to(dev), group)
-    assert np.array_equal(out.cpu().numpy(), oracle.rotate_f32(x.numpy(), group))
+    assert_same(out.cpu().numpy(), oracle.rotate_f32(x.numpy(), group))
 
 
 def gemv_bound(w, x, scale, half):
@@ -77,7 +77,7 @@ def test_rms_norm_bit_exact(dev, shape):
     w = (torch.randn(shape[-1], generator=g) * 0.1).float()  # gain ~ N(1, 0.1), stored zero-centred
     out = rms_norm.rms_norm(x.to(dev), w.to(dev), 1e-6)
     assert out.shape == x.shape and out.is_contiguous()
-    assert np.array_equal(bits(out), bits(oracle.rms_norm(x.numpy(), w.numpy(), 1e-6)))
+    assert_same(bits(out), bits(oracle.rms_norm(x.numpy(), w.numpy(), 1e-6)))
 
 
 def test_rms_norm_strided_heads(dev):
@@ -89,7 +89,7 @@ def test_rms_norm_strided_heads(dev):
     view = base.to(dev).view(B, L, H, D).transpose(1, 2)
     out = rms_norm.rms_norm(view, w.to(dev), 1e-6)
     ref = oracle.rms_norm(base.view(B, L, H, D).transpose(1, 2).contiguous().numpy(), w.numpy(), 1e-6)
-    assert np.array_equal(bits(out), bits(ref))
+    assert_same(bits(out), bits(ref))
 
 
 class _Norm:
@@ -109,4 +109,4 @@ def test_rms_norm_rope_bit_exact(dev, fb):
     xh = x.view(B, L, H, 128).transpose(1, 2).contiguous().numpy()
     f = freqs.numpy() if fb > 1 else np.broadcast_to(freqs.numpy(), (B,) + freqs.shape[1:])
     ref = oracle.rms_norm(xh, w.numpy(), 1e-6, freqs=np.ascontiguousarray(f))
-    assert np.array_equal(bits(out), bits(ref))
+    assert_same(bits(out), bits(ref))
