@@ -23,6 +23,9 @@ ARCH = "gfx950"
 # rounding points are the ones the code shows. Packed fp32 instructions are disabled.
 HIPFLAGS = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-source flags. attention.hip: MFMA results in VGPRs (the scores feed VALU softmax directly; with AGPR results
+# the compiler copies them out and spills the Q fragments).
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def torch_lib_dir():
@@ -36,7 +39,7 @@ def sources():
 
 def _compile(src, hipcc):
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc, *HIPFLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc, *HIPFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in (r.stderr or "").splitlines() if noise not in line)
