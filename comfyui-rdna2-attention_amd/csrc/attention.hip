@@ -7,34 +7,39 @@
 // hip_attention.hip:333-340); p = exp2(s * scale_log2 - m) (int8: exp2(s - m) with s already
 // scaled); l sums the fp32 p; P is rounded to fp16 before PV; out = fp16(o * (1 / l)).
 //
-// Work split. A workgroup of four wave64s owns 128 query rows of one (batch, head). The waves
-// form two pairs that walk the two halves of the key range; inside a pair each wave owns 64
-// query rows and keeps Q, O, l and m for them in registers. At the end the second pair's
-// (m, l, O) is merged into the first through LDS. With 128-row blocks the attention
-// configuration (24 heads x 4096 rows) is 768 workgroups, three per CU, one resident at a time.
-// Block ids are remapped so that the workgroups an XCD runs together belong to one head and
-// share its K/V through that XCD's L2.
+// Work split. A workgroup of eight wave64s owns 128 query rows of one (batch, head). The waves
+// form two groups of four that walk the two halves of the key range; inside a group each wave
+// owns 32 query rows and keeps Q, O, l and m for them in registers (about 200 VGPRs, so two
+// waves share each SIMD: one's softmax runs while the other's products keep the matrix core
+// busy). At the end the second group's (m, l, O) is merged into the first through LDS. With
+// 128-row blocks the attention configuration (24 heads x 4096 rows) is 768 workgroups, three per
+// CU, one resident at a time. Block ids are remapped so that the workgroups an XCD runs together
+// belong to one head and share its K/V through that XCD's L2.
 //
-// Tiles. Each pair stages 64-key tiles in its own double-buffered LDS: K row-major (pitch
-// 272 B, so the 16-byte reads of 16 consecutive keys hit distinct banks) and V transposed to
-// V^T[d][key] (pitch 144 B). Inside every 16-key group of a V^T row the keys are stored in the
-// order 0-3, 8-11, 4-7, 12-15: that is the order in which the S^T accumulator registers of
-// lane half g hold them, so each PV operand is one 16-byte read.
+// Tiles. Each group double-buffers 64-key tiles of K and V in LDS. They are copied by direct
+// global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes at LDS
+// base + 16 i), issued one whole tile ahead, so no register holds a tile in flight and the
+// load latency hides behind a full tile of work; the s_waitcnt before each tile's closing
+// barrier is where the next tile is awaited. Both tiles are row-major, 256 bytes per key
+// (int8 K: 128), with the 16-byte chunks of a row permuted by an XOR swizzle so that the
+// reads below hit distinct banks: K chunk c of key r sits at c ^ (r & 15) (int8: c ^ (r & 7)),
+// V chunk c at c ^ 4 (r & 3).
 //
 // Products. Scores are computed transposed, S^T = K Q^T (32x32x16 fp16 MFMA; 32x32x32 int8 for
 // int8-QK), so the accumulator registers of a lane all belong to its own query row (lane % 32)
-// and the row statistics need one exchange with lane ^ 32. O^T = V^T P^T then takes P straight
-// from those registers: in a 32x32 block lane l supplies row l % 32 of the A operand and column
-// l % 32 of B, k-half l / 32, and receives C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] in register r.
+// and the row statistics need one exchange with lane ^ 32 (v_permlane32_swap). O^T = V^T P^T
+// then takes P straight from those registers: in a 32x32 block lane l supplies row l % 32 of
+// the A operand and column l % 32 of B, k-half l / 32, and receives C[8 (r / 4) + 4 (l / 32) +
+// r % 4][l % 32] in register r. A lane's P operand for a 16-key step therefore holds keys
+// 4 g + {0-3, 8-11} (g = l / 32); the V^T operand is gathered in the same order from the
+// row-major V tile by two ds_read_b64_tr_b16, which hand lane i of each 16-lane group element
+// i % 4 of the 8-byte read of lane 4 e + i / 4 as its element e.
 #include "common.h"
 
-#define AT 256   // threads per workgroup: two pairs of waves
-#define PT 128   // threads per pair
-#define QB 128   // query rows per workgroup (64 per wave)
-#define KB 64    // keys per tile
-#define KP 272   // fp16 K tile row pitch (bytes)
-#define K8P 144  // int8 K tile row pitch
-#define VP 144   // V^T tile row pitch
+#define AT 512  // threads per workgroup: two groups of four waves
+#define GT 256  // threads per group
+#define QB 128  // query rows per workgroup (32 per wave)
+#define KB 64   // keys per tile
 
 struct AttnArgs {
     const half_t* q;
@@ -50,22 +55,38 @@ struct AttnArgs {
 
 template <bool I8>
 struct Tile {
-    static constexpr int K_BYTES = I8 ? KB * K8P + KB * 4 : KB * KP;
-    static constexpr int BYTES = K_BYTES + 128 * VP;  // one stage
-    static constexpr int PAIR = 2 * BYTES;            // two stages per pair
-    static constexpr int MERGE = 2 * 64 * 132 * 4;    // (O, m, l) of the second pair's two waves
-    static constexpr int LDS = 2 * PAIR > MERGE ? 2 * PAIR : MERGE;
+    static constexpr int K_ROW = I8 ? 128 : 256;
+    static constexpr int K_BYTES = KB * K_ROW + (I8 ? KB * 4 : 0);  // K rows, then the int8 per-key scales
+    static constexpr int BYTES = K_BYTES + KB * 256;                // one stage: K, then V
+    static constexpr int GROUP = 2 * BYTES;                         // two stages per group
+    static constexpr int MERGE_LANE = 68;                           // floats per lane: O (64), m, l, pad
+    static constexpr int MERGE = 4 * 64 * MERGE_LANE * 4;           // (O, m, l) of the second group's waves
+    static constexpr int LDS = 2 * GROUP > MERGE ? 2 * GROUP : MERGE;
 };
 
-// Byte offset, inside a V^T row, of the 4-key group kq (keys 4 kq .. 4 kq + 3) of a tile.
-__device__ __forceinline__ int vt_pos(int kq) { return (kq >> 2) * 32 + (kq & 1) * 16 + ((kq >> 1) & 1) * 8; }
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
+
+// Direct global->LDS copies: 16 (4) bytes per lane, lane i writing lds + 16 i (4 i).
+__device__ __forceinline__ void dma16(const void* src, char* lds) { __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds, 16, 0, 0); }
+__device__ __forceinline__ void dma4(const void* src, char* lds) { __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds, 4, 0, 0); }
+// Transposing 8-byte LDS read (see the header).
+__device__ __forceinline__ h4v read_tr(const char* lds) {
+    return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)lds));
+}
+// (x of lanes 0-31, x of lanes 32-63) for every lane: the two halves of a query row.
+__device__ __forceinline__ f2 halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return (f2){__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
 
 template <bool I8>
 __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
-    constexpr int TB = Tile<I8>::BYTES;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, g = lane >> 5, lq = lane & 31;
-    const int pair = t >> 7, pt = t & (PT - 1), wq = wave & 1;
+    using T = Tile<I8>;
+    const int t = threadIdx.x, lane = t & 63, g = lane >> 5, lq = lane & 31;
+    const int wave_u = __builtin_amdgcn_readfirstlane(t >> 6), wq = wave_u & 3, grp = wave_u >> 2;  // scalars
 
     // Block remap: consecutive block ids go round-robin to the 8 XCDs; give each XCD a contiguous run
     // of (head, q-block) work so its resident workgroups share K/V.
@@ -73,19 +94,18 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
     if (p.nblocks % 8 == 0) blk = (blk % 8) * (p.nblocks / 8) + blk / 8;
     const int bh = blk / p.qblocks, qblk = blk % p.qblocks;
     const int b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
-    const int q0 = qblk * QB + wq * 64;
+    const int q0 = qblk * QB + wq * 32;
 
-    // Q as the B operand of S^T = K Q^T, for the lane's two rows q0 + 32 qb + lq.
-    h8 qf[2][8];
-    i4v q8f[2][4];
-    float score_scale[2] = {p.scale_log2, p.scale_log2};
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const int qrow = min(q0 + qb * 32 + lq, p.Lq - 1);
+    // Q as the B operand of S^T = K Q^T, for the lane's row q0 + lq.
+    h8 qf[8];
+    i4v q8f[4];
+    float score_scale = p.scale_log2;
+    {
+        const int qrow = min(q0 + lq, p.Lq - 1);
         const half_t* qp = p.q + b * p.sqb + h * p.sqh + (long)qrow * p.sql;
         if (!I8) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) qf[qb][ks] = *(const h8*)(qp + ks * 16 + g * 8);
+            for (int ks = 0; ks < 8; ks++) qf[ks] = *(const h8*)(qp + ks * 16 + g * 8);
         } else {
             h8 raw[8];
             float qmax = 0.f;
@@ -98,9 +118,10 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
             for (int i = 0; i < 8; i++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) qmax = fmaxf(qmax, fabsf((float)raw[i][e]));
-            qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+            const f2 qh = halves(qmax);
+            qmax = fmaxf(qh[0], qh[1]);
             const float q_scale = fmaxf(qmax / 127.f, 1e-30f);  // hip_attention.hip:183
-            score_scale[qb] = q_scale * p.scale_log2;
+            score_scale = q_scale * p.scale_log2;
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 u4v w;
@@ -115,17 +136,15 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
                     }
                     w[d] = x;
                 }
-                q8f[qb][ks] = as_i4(w);
+                q8f[ks] = as_i4(w);
             }
         }
     }
 
-    f16v o[2][4];
+    f16v o[4];
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[qb][i] = (f16v){};
-    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
+    for (int i = 0; i < 4; i++) o[i] = (f16v){};
+    float m = -1e30f, l = 0.f;
 
     const half_t* kbase = p.k + b * p.skb + hk * p.skh;
     const half_t* vbase = p.v + b * p.svb + hk * p.svh;
@@ -134,229 +153,174 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
     const float* ksbase = I8 ? p.ks + (size_t)bkv * p.Lk_pad : nullptr;
 
     const int tiles = (p.Lk + KB - 1) / KB, half = (tiles + 1) / 2;
-    const int t_begin = pair * half, t_end = min(tiles, t_begin + half);
-    char* pbuf = smem + pair * Tile<I8>::PAIR;
+    const int t_begin = grp * half, t_end = min(tiles, t_begin + half);
+    char* gbuf = smem + grp * T::GROUP;
 
-    u4v rk[I8 ? 4 : 8], rv[8];
-    f4 rks = {};
-    // Global -> registers -> LDS stage buf, by the 128 threads of this pair, in two halves (K, then V) so
-    // that only one half of the next tile is held in registers at a time. Rows past Lk re-read row
-    // Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite) values drop out.
-    auto load_k = [&](int key0) {
-        if (!I8) {
+    // Copies the tile at key0 into stage st; the group's four waves take every fourth 1 KiB block, so
+    // DMA i of a wave fills K (and V) rows 16 i + row0 .. +3, row0 = 4 wq + lane / 16. Rows past Lk
+    // re-read row Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite) values
+    // drop out. int8 K is zero-padded to a whole tile by pack_k_i8. Per-lane byte offsets are fixed;
+    // only the tile base moves (the launcher keeps 64 rows of stride inside 2^31 bytes).
+    const int row0 = 4 * wq + (lane >> 4);
+    const long skl2 = p.skl * 2, svl2 = p.svl * 2;
+    const int kc = (lane & 15) ^ row0, vc = (lane & 15) ^ ((lane >> 4) << 2);
+    const u32 k_off = (u32)(row0 * skl2) + ((u32)kc << 4);
+    const u32 v_off = (u32)(row0 * svl2) + ((u32)vc << 4);
+    const u32 k8_off = (u32)((8 * wq + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
+    auto issue = [&](int key0, char* st) {
+        if (I8) {
+            const char* kt = (const char*)k8base + (size_t)key0 * 128;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = pt + i * PT, key = c >> 4, dc = c & 15;
-                rk[i] = *(const u4v*)(kbase + (long)min(key0 + key, p.Lk - 1) * p.skl + dc * 8);
+            for (int i = 0; i < 2; i++) dma16(kt + i * 4096 + k8_off, st + (4 * i + wq) * 1024);
+            if (wq == 0) dma4(ksbase + key0 + lane, st + KB * 128);
+        }
+        if (key0 + KB <= p.Lk) {
+            const char* kt = (const char*)kbase + key0 * skl2;
+            const char* vt = (const char*)vbase + key0 * svl2;
+            if (!I8) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) dma16(kt + i * 16 * skl2 + k_off, st + (4 * i + wq) * 1024);
             }
+#pragma unroll
+            for (int i = 0; i < 4; i++) dma16(vt + i * 16 * svl2 + v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int c = pt + i * PT, key = c >> 3, dc = c & 7;
-                rk[i] = *(const u4v*)(k8base + (size_t)(key0 + key) * 128 + dc * 16);
+                const int key = min(key0 + 16 * i + row0, p.Lk - 1);
+                if (!I8) dma16(kbase + (long)key * p.skl + kc * 8, st + (4 * i + wq) * 1024);
+                dma16(vbase + (long)key * p.svl + vc * 8, st + T::K_BYTES + (4 * i + wq) * 1024);
             }
-            if (pt < 16) rks = *(const f4*)(ksbase + key0 + pt * 4);
-        }
-    };
-    auto store_k = [&](int buf) {
-        char* st = pbuf + buf * TB;
-        if (!I8) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int c = pt + i * PT, key = c >> 4, dc = c & 15;
-                *(u4v*)(st + key * KP + dc * 16) = rk[i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int c = pt + i * PT, key = c >> 3, dc = c & 7;
-                *(u4v*)(st + key * K8P + dc * 16) = rk[i];
-            }
-            if (pt < 16) *(f4*)(st + KB * K8P + pt * 16) = rks;
-        }
-    };
-    // V: unit u = (4-key group kq = u % 16, 8-dim group dq = u / 16), two units per thread.
-    auto load_v = [&](int key0) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int u = pt + j * PT, kq = u & 15, dq = u >> 4;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int key = min(key0 + kq * 4 + i, p.Lk - 1);
-                rv[j * 4 + i] = *(const u4v*)(vbase + (long)key * p.svl + dq * 8);
-            }
-        }
-    };
-    auto store_v = [&](int buf) {
-        char* vt = pbuf + buf * TB + Tile<I8>::K_BYTES;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int u = pt + j * PT, kq = u & 15, dq = u >> 4;
-            const h8 v0 = __builtin_bit_cast(h8, rv[j * 4]), v1 = __builtin_bit_cast(h8, rv[j * 4 + 1]);
-            const h8 v2 = __builtin_bit_cast(h8, rv[j * 4 + 2]), v3 = __builtin_bit_cast(h8, rv[j * 4 + 3]);
-            char* col = vt + vt_pos(kq);
-#pragma unroll
-            for (int e = 0; e < 8; e++) *(h4v*)(col + (dq * 8 + e) * VP) = (h4v){v0[e], v1[e], v2[e], v3[e]};
         }
     };
 
-    if (t_begin < t_end) {
-        load_k(t_begin * KB);
-        store_k(0);
-        load_v(t_begin * KB);
-        store_v(0);
-    }
+    // Per-lane parts of the V^T operand addresses: key row 16 j + 8 s + vrow, chunk (4 dt + vchunk) ^ vswz.
+    const int sig = lane & 15, vrow = 4 * g + (sig >> 2), vchunk = 2 * ((lane >> 4) & 1) + ((sig & 3) >> 1), vswz = (sig >> 2) << 2;
+    const int vbyte = (sig & 1) * 8;
+
+    if (t_begin < t_end) issue(t_begin * KB, gbuf);
     __syncthreads();
-    // Both pairs run the same number of iterations (the second may have one tile fewer) so that
+    // Both groups run the same number of iterations (the second may have one tile fewer) so that
     // every wave reaches every barrier.
     for (int it = 0; it < half; it++) {
         const int tile = t_begin + it;
         const bool active = tile < t_end, next = active && tile + 1 < t_end;
-        const int buf = it & 1, key0 = tile * KB;
+        const int key0 = tile * KB;
+        const char* st = gbuf + (it & 1) * T::BYTES;
+        if (next) issue(key0 + KB, gbuf + ((it + 1) & 1) * T::BYTES);
         if (active) {
-            if (next) load_k(key0 + KB);
-            __builtin_amdgcn_sched_barrier(0);
-            const char* st = pbuf + buf * TB;
-            float s[2][2][16];  // [qb][kb][r]
+            float s[2][16];  // [kb][r]
             if (!I8) {
+                f16v acc[2] = {};
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    f16v acc[2] = {};
+                for (int ks = 0; ks < 8; ks++)
 #pragma unroll
-                    for (int ks = 0; ks < 8; ks++) {
-                        const h8 a = *(const h8*)(st + (kb * 32 + lq) * KP + ks * 32 + g * 16);
-                        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[0][ks], acc[0], 0, 0, 0);
-                        acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[1][ks], acc[1], 0, 0, 0);
+                    for (int kb = 0; kb < 2; kb++) {
+                        const h8 a = *(const h8*)(st + (kb * 32 + lq) * 256 + (((2 * ks + g) ^ (lq & 15)) << 4));
+                        acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], acc[kb], 0, 0, 0);
                     }
 #pragma unroll
-                    for (int qb = 0; qb < 2; qb++)
+                for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                        for (int r = 0; r < 16; r++) s[qb][kb][r] = acc[qb][r];
-                }
+                    for (int r = 0; r < 16; r++) s[kb][r] = acc[kb][r];
             } else {
-                const float* kscale = (const float*)(st + KB * K8P);
+                const float* kscale = (const float*)(st + KB * 128);
+                i16v acc[2] = {};
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++) {
-                    i16v acc[2] = {};
+                for (int ks = 0; ks < 4; ks++)
 #pragma unroll
-                    for (int ks = 0; ks < 4; ks++) {
-                        const i4v a = *(const i4v*)(st + (kb * 32 + lq) * K8P + ks * 32 + g * 16);
-                        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q8f[0][ks], acc[0], 0, 0, 0);
-                        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q8f[1][ks], acc[1], 0, 0, 0);
+                    for (int kb = 0; kb < 2; kb++) {
+                        const i4v a = *(const i4v*)(st + (kb * 32 + lq) * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+                        acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q8f[ks], acc[kb], 0, 0, 0);
                     }
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                     for (int r4 = 0; r4 < 4; r4++) {
                         const f4 sc = *(const f4*)(kscale + kb * 32 + 8 * r4 + 4 * g);
 #pragma unroll
-                        for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-                            for (int e = 0; e < 4; e++)
-                                s[qb][kb][r4 * 4 + e] = (float)acc[qb][r4 * 4 + e] * score_scale[qb] * sc[e];  // hip_attention.hip:227
+                        for (int e = 0; e < 4; e++) s[kb][r4 * 4 + e] = (float)acc[kb][r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
                     }
-                }
             }
-            __builtin_amdgcn_sched_barrier(0);
-            if (next) store_k(buf ^ 1);
             // Keys past Lk (hip_attention.hip:324-328).
             if (key0 + KB > p.Lk) {
 #pragma unroll
                 for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                     for (int r = 0; r < 16; r++)
-                        if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) {
-                            s[0][kb][r] = -1e30f;
-                            s[1][kb][r] = -1e30f;
-                        }
+                        if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[kb][r] = -1e30f;
             }
-            float mx[2];
+            float mx = s[0][0];
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++) {
-                float v = s[qb][0][0];
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
+            const f2 mh = halves(mx);
+            mx = fmaxf(mh[0], mh[1]);
+            if (!I8) mx *= p.scale_log2;
+            if (__any(mx > m + 8.f)) {
+                const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
+                m = mn;
+                l *= alpha;
 #pragma unroll
-                    for (int r = 0; r < 16; r++) v = fmaxf(v, s[qb][kb][r]);
-                v = fmaxf(v, __shfl_xor(v, 32, 64));
-                mx[qb] = I8 ? v : v * p.scale_log2;
-            }
-            if (__any(mx[0] > m[0] + 8.f || mx[1] > m[1] + 8.f)) {
-#pragma unroll
-                for (int qb = 0; qb < 2; qb++) {
-                    const float mn = fmaxf(m[qb], mx[qb]), alpha = __builtin_amdgcn_exp2f(m[qb] - mn);
-                    m[qb] = mn;
-                    l[qb] *= alpha;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) o[qb][i] *= alpha;
-                }
+                for (int i = 0; i < 4; i++) o[i] *= alpha;
             }
             // P, packed for the four 16-key steps: step j holds registers 8 (j % 2) .. +8 of block j / 2.
-            h8 pf[2][4];
+            h8 pf[4];
 #pragma unroll
-            for (int qb = 0; qb < 2; qb++)
+            for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int r = 0; r < 16; r += 2) {
-                        const float e0 = I8 ? __builtin_amdgcn_exp2f(s[qb][kb][r] - m[qb]) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][kb][r], p.scale_log2, -m[qb]));
-                        const float e1 = I8 ? __builtin_amdgcn_exp2f(s[qb][kb][r + 1] - m[qb])
-                                            : __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][kb][r + 1], p.scale_log2, -m[qb]));
-                        l[qb] += e0 + e1;
-                        const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
-                        pf[qb][kb * 2 + (r >> 3)][r & 7] = pk[0];
-                        pf[qb][kb * 2 + (r >> 3)][(r & 7) + 1] = pk[1];
-                    }
+                for (int r = 0; r < 16; r += 2) {
+                    const float e0 = I8 ? __builtin_amdgcn_exp2f(s[kb][r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.scale_log2, -m));
+                    const float e1 = I8 ? __builtin_amdgcn_exp2f(s[kb][r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], p.scale_log2, -m));
+                    l += e0 + e1;
+                    const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
+                    pf[kb * 2 + (r >> 3)][r & 7] = pk[0];
+                    pf[kb * 2 + (r >> 3)][(r & 7) + 1] = pk[1];
+                }
 
-            __builtin_amdgcn_sched_barrier(0);
-            if (next) load_v(key0 + KB);
             // O^T += V^T P^T.
-            const char* vt = st + Tile<I8>::K_BYTES;
+            const char* vt = st + T::K_BYTES;
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++) {
-                    const h8 a = *(const h8*)(vt + (dt * 32 + lq) * VP + j * 32 + g * 16);
-                    o[0][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[0][j], o[0][dt], 0, 0, 0);
-                    o[1][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[1][j], o[1][dt], 0, 0, 0);
+                    const char* va = vt + (16 * j + vrow) * 256 + (((4 * dt + vchunk) ^ vswz) << 4) + vbyte;
+                    const h4v lo = read_tr(va), hi = read_tr(va + 8 * 256);
+                    const h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[j], o[dt], 0, 0, 0);
                 }
-            if (next) store_v(buf ^ 1);
         }
-        __syncthreads();
+        __syncthreads();  // waits for this wave's copies of the next tile, then for every wave
     }
 
-    // Merge the second pair's (m, l, O) into the first pair's, then normalise and store.
-    float* mb = (float*)smem + (wq * 64 + lane) * 132;
-    if (pair == 1) {
-#pragma unroll
-        for (int qb = 0; qb < 2; qb++) {
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r += 4) *(f4*)(mb + qb * 64 + dt * 16 + r) = (f4){o[qb][dt][r], o[qb][dt][r + 1], o[qb][dt][r + 2], o[qb][dt][r + 3]};
-            mb[128 + qb * 2] = m[qb];
-            mb[129 + qb * 2] = l[qb];
-        }
-    }
-    __syncthreads();
-    if (pair == 1) return;
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-        const float m1 = mb[128 + qb * 2], l1 = mb[129 + qb * 2];
-        const float mn = fmaxf(m[qb], m1), a0 = __builtin_amdgcn_exp2f(m[qb] - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
-        const float lsum = l[qb] * a0 + l1 * a1;
-        const float inv = 1.f / (lsum + __shfl_xor(lsum, 32, 64));  // the lane halves hold disjoint keys of one row
-        const int row = q0 + qb * 32 + lq;
-        half_t* op = p.o + b * p.sob + h * p.soh + (long)row * p.sol;
+    // Merge the second group's (m, l, O) into the first group's, then normalise and store.
+    float* mb = (float*)smem + (wq * 64 + lane) * T::MERGE_LANE;
+    if (grp == 1) {
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const f4 o1 = *(const f4*)(mb + qb * 64 + dt * 16 + r4 * 4);
-                h4v w;
-#pragma unroll
-                for (int e = 0; e < 4; e++) w[e] = to_half((o[qb][dt][r4 * 4 + e] * a0 + o1[e] * a1) * inv);
-                if (row < p.Lq) *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
-            }
+            for (int r = 0; r < 16; r += 4) *(f4*)(mb + dt * 16 + r) = (f4){o[dt][r], o[dt][r + 1], o[dt][r + 2], o[dt][r + 3]};
+        mb[64] = m;
+        mb[65] = l;
     }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = mb[64], l1 = mb[65];
+    const float mn = fmaxf(m, m1), a0 = __builtin_amdgcn_exp2f(m - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
+    const f2 lh = halves(l * a0 + l1 * a1);
+    const float inv = 1.f / (lh[0] + lh[1]);  // the lane halves hold disjoint keys of one row
+    const int row = q0 + lq;
+    half_t* op = p.o + b * p.sob + h * p.soh + (long)row * p.sol;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+            const f4 o1 = *(const f4*)(mb + dt * 16 + r4 * 4);
+            h4v w;
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = to_half((o[dt][r4 * 4 + e] * a0 + o1[e] * a1) * inv);
+            if (row < p.Lq) *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
+        }
 }
 
 // Per-key absmax int8 quantization of K (pack_kv_i8, hip_attention.hip:56-94): 16 lanes per key,
@@ -430,8 +394,10 @@ static int launch_attn(const AttnArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-static bool attn_shapes_ok(int B, int H, int Hkv, int Lq, int Lk) {
-    return B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && Lq > 0 && Lk > 0 && (long)B * H * ((Lq + QB - 1) / QB) < (1L << 31);
+// Row strides of K and V must keep a tile's 64 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
+static bool attn_shapes_ok(int B, int H, int Hkv, int Lq, int Lk, const long* st) {
+    const bool rows_ok = st[5] >= 0 && st[5] < (1L << 24) && st[8] >= 0 && st[8] < (1L << 24);
+    return B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && Lq > 0 && Lk > 0 && (long)B * H * ((Lq + QB - 1) / QB) < (1L << 31) && rows_ok;
 }
 
 extern "C" {
@@ -443,7 +409,7 @@ size_t rda_attn_i8_workspace(int B, int Hkv, int Lk) {
 
 int rda_attn(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
              void* stream) {
-    if (!attn_shapes_ok(B, H, Hkv, Lq, Lk)) return RDA_ERR_INVALID;
+    if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
     return launch_attn<false>(make_args(q, k, v, out, B, H, Hkv, Lq, Lk, strides, scale), stream);
 }
 
@@ -459,7 +425,7 @@ int rda_pack_k_i8(const void* k, void* workspace, int B, int Hkv, int Lk, long s
 
 int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
                 float scale, void* stream) {
-    if (!attn_shapes_ok(B, H, Hkv, Lq, Lk)) return RDA_ERR_INVALID;
+    if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
     AttnArgs a = make_args(q, nullptr, v, out, B, H, Hkv, Lq, Lk, strides, scale);
     a.k8 = (const int8_t*)workspace;
     a.ks = (const float*)(a.k8 + (size_t)B * Hkv * a.Lk_pad * 128);
