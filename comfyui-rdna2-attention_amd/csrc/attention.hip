@@ -58,19 +58,32 @@ struct Tile {
     static constexpr int K_ROW = I8 ? 128 : 256;
     static constexpr int K_BYTES = KB * K_ROW + (I8 ? KB * 4 : 0);  // K rows, then the int8 per-key scales
     static constexpr int BYTES = K_BYTES + KB * 256;                // one stage: K, then V
-    static constexpr int GROUP = 2 * BYTES;                         // two stages per group
+    static constexpr int STAGES = 4 * BYTES;                        // two stages per group
     static constexpr int MERGE_LANE = 68;                           // floats per lane: O (64), m, l, pad
     static constexpr int MERGE = 4 * 64 * MERGE_LANE * 4;           // (O, m, l) of the second group's waves
-    static constexpr int LDS = 2 * GROUP > MERGE ? 2 * GROUP : MERGE;
+    static constexpr int LDS = STAGES > MERGE ? STAGES : MERGE;
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
 
-// Direct global->LDS copies: 16 (4) bytes per lane, lane i writing lds + 16 i (4 i).
-__device__ __forceinline__ void dma16(const void* src, char* lds) { __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds, 16, 0, 0); }
-__device__ __forceinline__ void dma4(const void* src, char* lds) { __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds, 4, 0, 0); }
+// Direct global->LDS copies: 16 (4) bytes per lane from base + off (or from src), lane i writing LDS
+// address lds + 16 i (4 i). They are issued from asm, which keeps them out of the compiler's wait
+// bookkeeping: the compiler cannot tell the LDS they fill from the stage the products read and would
+// otherwise make those reads wait for the next tile's copies. The kernel waits for them itself
+// (wait_copies) before the barrier that hands a stage over.
+__device__ __forceinline__ u32 lds_addr(const char* p) { return (u32)(uintptr_t)(const lds_void_t*)p; }
+__device__ __forceinline__ void dma16(const void* base, u32 off, const char* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, u32 off, const char* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_at(const void* src, const char* lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Transposing 8-byte LDS read (see the header).
 __device__ __forceinline__ h4v read_tr(const char* lds) {
     return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)lds));
@@ -82,14 +95,14 @@ __device__ __forceinline__ f2 halves(float x) {
 }
 
 template <bool I8>
-__global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
+__global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel(AttnArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     using T = Tile<I8>;
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, lq = lane & 31;
     const int wave_u = __builtin_amdgcn_readfirstlane(t >> 6), wq = wave_u & 3, grp = wave_u >> 2;  // scalars
 
     // Block remap: consecutive block ids go round-robin to the 8 XCDs; give each XCD a contiguous run
-    // of (head, q-block) work so its resident workgroups share K/V.
+    // of (head, q-block) work so its resident workgroups share K/V through its L2.
     int blk = blockIdx.x;
     if (p.nblocks % 8 == 0) blk = (blk % 8) * (p.nblocks / 8) + blk / 8;
     const int bh = blk / p.qblocks, qblk = blk % p.qblocks;
@@ -105,7 +118,10 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
         const half_t* qp = p.q + b * p.sqb + h * p.sqh + (long)qrow * p.sql;
         if (!I8) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) qf[ks] = *(const h8*)(qp + ks * 16 + g * 8);
+            for (int ks = 0; ks < 8; ks++) {
+                qf[ks] = *(const h8*)(qp + ks * 16 + g * 8);
+                asm volatile("" : "+v"(qf[ks]));  // the loads complete here, not inside the tile loop
+            }
         } else {
             h8 raw[8];
             float qmax = 0.f;
@@ -154,7 +170,6 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
 
     const int tiles = (p.Lk + KB - 1) / KB, half = (tiles + 1) / 2;
     const int t_begin = grp * half, t_end = min(tiles, t_begin + half);
-    char* gbuf = smem + grp * T::GROUP;
 
     // Copies the tile at key0 into stage st; the group's four waves take every fourth 1 KiB block, so
     // DMA i of a wave fills K (and V) rows 16 i + row0 .. +3, row0 = 4 wq + lane / 16. Rows past Lk
@@ -167,131 +182,173 @@ __global__ __launch_bounds__(AT, 1) void attn_kernel(AttnArgs p) {
     const u32 k_off = (u32)(row0 * skl2) + ((u32)kc << 4);
     const u32 v_off = (u32)(row0 * svl2) + ((u32)vc << 4);
     const u32 k8_off = (u32)((8 * wq + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
-    auto issue = [&](int key0, char* st) {
+    auto issue = [&](int key0, const char* st) {
         if (I8) {
             const char* kt = (const char*)k8base + (size_t)key0 * 128;
 #pragma unroll
-            for (int i = 0; i < 2; i++) dma16(kt + i * 4096 + k8_off, st + (4 * i + wq) * 1024);
-            if (wq == 0) dma4(ksbase + key0 + lane, st + KB * 128);
+            for (int i = 0; i < 2; i++) dma16(kt + i * 4096, k8_off, st + (4 * i + wq) * 1024);
+            if (wq == 0) dma4(ksbase + key0, lane * 4, st + KB * 128);
         }
         if (key0 + KB <= p.Lk) {
             const char* kt = (const char*)kbase + key0 * skl2;
             const char* vt = (const char*)vbase + key0 * svl2;
             if (!I8) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) dma16(kt + i * 16 * skl2 + k_off, st + (4 * i + wq) * 1024);
+                for (int i = 0; i < 4; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + wq) * 1024);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) dma16(vt + i * 16 * svl2 + v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
+            for (int i = 0; i < 4; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int key = min(key0 + 16 * i + row0, p.Lk - 1);
-                if (!I8) dma16(kbase + (long)key * p.skl + kc * 8, st + (4 * i + wq) * 1024);
-                dma16(vbase + (long)key * p.svl + vc * 8, st + T::K_BYTES + (4 * i + wq) * 1024);
+                if (!I8) dma16_at(kbase + (long)key * p.skl + kc * 8, st + (4 * i + wq) * 1024);
+                dma16_at(vbase + (long)key * p.svl + vc * 8, st + T::K_BYTES + (4 * i + wq) * 1024);
             }
         }
     };
 
-    // Per-lane parts of the V^T operand addresses: key row 16 j + 8 s + vrow, chunk (4 dt + vchunk) ^ vswz.
-    const int sig = lane & 15, vrow = 4 * g + (sig >> 2), vchunk = 2 * ((lane >> 4) & 1) + ((sig & 3) >> 1), vswz = (sig >> 2) << 2;
-    const int vbyte = (sig & 1) * 8;
-
-    if (t_begin < t_end) issue(t_begin * KB, gbuf);
-    __syncthreads();
-    // Both groups run the same number of iterations (the second may have one tile fewer) so that
-    // every wave reaches every barrier.
-    for (int it = 0; it < half; it++) {
-        const int tile = t_begin + it;
-        const bool active = tile < t_end, next = active && tile + 1 < t_end;
-        const int key0 = tile * KB;
-        const char* st = gbuf + (it & 1) * T::BYTES;
-        if (next) issue(key0 + KB, gbuf + ((it + 1) & 1) * T::BYTES);
-        if (active) {
-            float s[2][16];  // [kb][r]
-            if (!I8) {
-                f16v acc[2] = {};
+    // S^T of the tile in stage st (scaled for int8), into s.
+    float s[2][16];  // [kb][r]
+    auto scores = [&](const char* st) {
+        if (!I8) {
+            // K operands in two batches of eight reads; each batch goes out before the products that use it.
+            // Lane-dependent parts of the addresses are recomputed here from an opaque copy of the lane id:
+            // hoisted out of the tile loop they would hold a dozen VGPRs for its whole length.
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            const char* krow = st + (ln & 31) * 256;
+            const int kx = (ln & 15) ^ (ln >> 5);  // chunk 2 ks + g sits at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx
+            f16v acc[2] = {};
 #pragma unroll
-                for (int ks = 0; ks < 8; ks++)
+            for (int half_k = 0; half_k < 2; half_k++) {
+                h8 ka[4][2];
+#pragma unroll
+                for (int k4 = 0; k4 < 4; k4++)
 #pragma unroll
                     for (int kb = 0; kb < 2; kb++) {
-                        const h8 a = *(const h8*)(st + (kb * 32 + lq) * 256 + (((2 * ks + g) ^ (lq & 15)) << 4));
-                        acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[ks], acc[kb], 0, 0, 0);
+                        const int ks = half_k * 4 + k4;
+                        ka[k4][kb] = *(const h8*)(krow + kb * 32 * 256 + (((2 * ks) ^ kx) << 4));
                     }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++)
+                for (int k4 = 0; k4 < 4; k4++)
 #pragma unroll
-                    for (int r = 0; r < 16; r++) s[kb][r] = acc[kb][r];
-            } else {
-                const float* kscale = (const float*)(st + KB * 128);
-                i16v acc[2] = {};
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                    for (int kb = 0; kb < 2; kb++) {
-                        const i4v a = *(const i4v*)(st + (kb * 32 + lq) * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
-                        acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, q8f[ks], acc[kb], 0, 0, 0);
-                    }
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int r4 = 0; r4 < 4; r4++) {
-                        const f4 sc = *(const f4*)(kscale + kb * 32 + 8 * r4 + 4 * g);
-#pragma unroll
-                        for (int e = 0; e < 4; e++) s[kb][r4 * 4 + e] = (float)acc[kb][r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
-                    }
+                    for (int kb = 0; kb < 2; kb++) acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4][kb], qf[half_k * 4 + k4], acc[kb], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            // Keys past Lk (hip_attention.hip:324-328).
-            if (key0 + KB > p.Lk) {
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[kb][r] = -1e30f;
-            }
-            float mx = s[0][0];
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
-            const f2 mh = halves(mx);
-            mx = fmaxf(mh[0], mh[1]);
-            if (!I8) mx *= p.scale_log2;
-            if (__any(mx > m + 8.f)) {
-                const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
-                m = mn;
-                l *= alpha;
+                for (int r = 0; r < 16; r++) s[kb][r] = acc[kb][r];
+        } else {
+            const float* kscale = (const float*)(st + KB * 128);
+            i4v ka[4][2];
 #pragma unroll
-                for (int i = 0; i < 4; i++) o[i] *= alpha;
-            }
-            // P, packed for the four 16-key steps: step j holds registers 8 (j % 2) .. +8 of block j / 2.
-            h8 pf[4];
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) ka[ks][kb] = *(const i4v*)(st + (kb * 32 + lq) * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+            __builtin_amdgcn_sched_barrier(0);
+            i16v acc[2] = {};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks][kb], q8f[ks], acc[kb], 0, 0, 0);
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-                for (int r = 0; r < 16; r += 2) {
-                    const float e0 = I8 ? __builtin_amdgcn_exp2f(s[kb][r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.scale_log2, -m));
-                    const float e1 = I8 ? __builtin_amdgcn_exp2f(s[kb][r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], p.scale_log2, -m));
-                    l += e0 + e1;
-                    const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
-                    pf[kb * 2 + (r >> 3)][r & 7] = pk[0];
-                    pf[kb * 2 + (r >> 3)][(r & 7) + 1] = pk[1];
-                }
-
-            // O^T += V^T P^T.
-            const char* vt = st + T::K_BYTES;
+                for (int r4 = 0; r4 < 4; r4++) {
+                    const f4 sc = *(const f4*)(kscale + kb * 32 + 8 * r4 + 4 * g);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const char* va = vt + (16 * j + vrow) * 256 + (((4 * dt + vchunk) ^ vswz) << 4) + vbyte;
-                    const h4v lo = read_tr(va), hi = read_tr(va + 8 * 256);
-                    const h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[j], o[dt], 0, 0, 0);
+                    for (int e = 0; e < 4; e++) s[kb][r4 * 4 + e] = (float)acc[kb][r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
                 }
         }
-        __syncthreads();  // waits for this wave's copies of the next tile, then for every wave
+    };
+    // Masking, the online softmax and O^T += V^T P^T for the tile at key0 in stage st, from s.
+    auto update = [&](const char* st, int key0) {
+        // Keys past Lk (hip_attention.hip:324-328).
+        if (key0 + KB > p.Lk) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[kb][r] = -1e30f;
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
+        const f2 mh = halves(mx);
+        mx = fmaxf(mh[0], mh[1]);
+        if (!I8) mx *= p.scale_log2;
+        if (__any(mx > m + 8.f)) {
+            const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] *= alpha;
+        }
+        // V^T operands in four batches of four products; the first batch goes out before the P arithmetic,
+        // which hides its latency, each later one before the products of the batch ahead of it.
+        int ln = lane;  // opaque lane id, as in scores
+        asm volatile("" : "+v"(ln));
+        const int sg = ln & 15;
+        const char* vt = st + T::K_BYTES + (4 * (ln >> 5) + (sg >> 2)) * 256 + (sg & 1) * 8;
+        const int vx = (2 * ((ln >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
+        auto read_v = [&](h8 (&va)[4], int j) {
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const char* ra = vt + 16 * j * 256 + (((4 * dt) ^ vx) << 4);
+                va[dt] = __builtin_shufflevector(read_tr(ra), read_tr(ra + 8 * 256), 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        };
+        h8 va[2][4];
+        read_v(va[0], 0);
+        __builtin_amdgcn_sched_barrier(0);
+        // P, packed for the four 16-key steps: step j holds registers 8 (j % 2) .. +8 of block j / 2.
+        h8 pf[4];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+                const float e0 = I8 ? __builtin_amdgcn_exp2f(s[kb][r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.scale_log2, -m));
+                const float e1 = I8 ? __builtin_amdgcn_exp2f(s[kb][r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], p.scale_log2, -m));
+                l += e0 + e1;
+                const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
+                pf[kb * 2 + (r >> 3)][r & 7] = pk[0];
+                pf[kb * 2 + (r >> 3)][(r & 7) + 1] = pk[1];
+            }
+        // O^T += V^T P^T.
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j < 3) read_v(va[(j + 1) & 1], j + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[j & 1][dt], pf[j], o[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Tile loop: the copies of tile i + 1 go out before the work on tile i and are awaited at its closing
+    // barrier, which also retires every read of the stage the next copies overwrite. Both groups run
+    // `half` iterations (the second may have one tile fewer) so that every wave reaches every barrier.
+    const int n = t_end - t_begin;  // tiles of this group: half for group 0, half or half - 1 for group 1
+    const char* gbuf = smem + grp * 2 * T::BYTES;
+    auto stage = [&](int i) -> const char* { return gbuf + (i & 1) * T::BYTES; };
+    if (n > 0) issue(t_begin * KB, stage(0));
+    wait_copies();
+    __syncthreads();
+    for (int i = 0; i < half; i++) {
+        if (i < n) {
+            if (i + 1 < n) issue((t_begin + i + 1) * KB, stage(i + 1));
+            scores(stage(i));
+            update(stage(i), (t_begin + i) * KB);
+        }
+        wait_copies();
+        __syncthreads();
     }
+    __syncthreads();  // every stage read retires before the merge area (which overlaps the stages) is written
 
     // Merge the second group's (m, l, O) into the first group's, then normalise and store.
     float* mb = (float*)smem + (wq * 64 + lane) * T::MERGE_LANE;
