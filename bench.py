@@ -6,8 +6,8 @@ timed steps (4 B H S^2 D = 206.16 GFLOP per step). The other configurations of t
 GEMM TOPS), int8-QK attention, the W4A8 linear, the DiT MLP tail and the decode GEMV / attention (HBM GB/s) -- are
 measured in the same run and reported under "components".
 
-Timing: every launch is bracketed by HIP events on torch's current stream (the stream the library launches on);
-`roofline.achieved` = algorithmic work / mean kernel time. Kernels shorter than ~50 us are timed by replaying a
+Timing: the timed steps run back to back between two HIP events on torch's current stream (the stream the
+library launches on); `roofline.achieved` = algorithmic work / mean time per step. Kernels shorter than ~50 us are timed by replaying a
 captured HIP graph of many launches, so host launch overhead does not stretch them. HBM-bound kernels rotate over
 more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve them. The CPU baseline is the
 reference's attention fallback (attention_bmm: chunked baddbmm -> softmax -> bmm, attention.py:15-43) on the host
@@ -56,21 +56,20 @@ def gen(torch, seed):
 
 
 def event_timed(torch, fn, steps, warmup, copies=1):
-    """warmup + steps calls of fn(i); returns (wall ms per step, mean ms between the events around each call)."""
+    """warmup + steps calls of fn(i), back to back; returns (wall ms per step, ms per step between two HIP events
+    recorded on torch's current stream -- the stream the library launches on -- around the timed region)."""
     for i in range(warmup):
         fn(i % copies)
     torch.cuda.synchronize()
-    pairs = []
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    s.record()
     for i in range(steps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
         fn(i % copies)
-        e.record()
-        pairs.append((s, e))
+    e.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    return wall, sum(s.elapsed_time(e) for s, e in pairs) / steps
+    return wall, s.elapsed_time(e) / steps
 
 
 def graph_timed(torch, fn, steps, warmup, copies=1):
@@ -277,7 +276,7 @@ def run_workload(torch, dev, name, steps, warmup, traffic):
     kind, peak, unit = PEAKS[bound]
     achieved = work / kms / 1e9 if kind == "mfma" else work / kms / 1e6
     rec = {"value": round(achieved, 1), "unit": "TOP/s" if bound == "mfma_i8" else unit, "kernel_ms": round(kms, 5), "wall_ms": round(wall, 5),
-           "roofline": roofline(kind, achieved, peak, unit, traffic.get(name)), "timing": "hip-graph replay" if timer is graph_timed else "per-launch events"}
+           "roofline": roofline(kind, achieved, peak, unit, traffic.get(name)), "timing": "hip-graph replay" if timer is graph_timed else "events around back-to-back launches"}
     log(f"{name}: {rec['value']} {rec['unit']} ({kms * 1e3:.2f} us, {rec['roofline']['frac'] * 100:.1f}% of peak)")
     return rec
 
