@@ -64,26 +64,9 @@ struct Tile {
     static constexpr int LDS = STAGES > MERGE ? STAGES : MERGE;
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
 
-// Direct global->LDS copies: 16 (4) bytes per lane from base + off (or from src), lane i writing LDS
-// address lds + 16 i (4 i). They are issued from asm, which keeps them out of the compiler's wait
-// bookkeeping: the compiler cannot tell the LDS they fill from the stage the products read and would
-// otherwise make those reads wait for the next tile's copies. The kernel waits for them itself
-// (wait_copies) before the barrier that hands a stage over.
-__device__ __forceinline__ u32 lds_addr(const char* p) { return (u32)(uintptr_t)(const lds_void_t*)p; }
-__device__ __forceinline__ void dma16(const void* base, u32 off, const char* lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* base, u32 off, const char* lds) {
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_at(const void* src, const char* lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
-}
-__device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Transposing 8-byte LDS read (see the header).
 __device__ __forceinline__ h4v read_tr(const char* lds) {
     return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)lds));

@@ -93,3 +93,25 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __device__ __forceinline__ i4v as_i4(u4v v) { return __builtin_bit_cast(i4v, v); }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Direct global->LDS copies: 16 (4) bytes per lane from base + off (or from src), lane i writing LDS
+// address lds + 16 i (4 i). They are issued from asm, which keeps them out of the compiler's wait
+// bookkeeping: the compiler cannot tell the LDS stage they fill from the stage being read and would
+// otherwise make every LDS read wait for the copies in flight. A kernel waits for its copies itself
+// (wait_copies, wait_copies_but) before the barrier that hands a stage over.
+__device__ __forceinline__ u32 lds_addr(const char* p) { return (u32)(uintptr_t)(const lds_void_t*)p; }
+__device__ __forceinline__ void dma16(const void* base, u32 off, const char* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, u32 off, const char* lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_at(const void* src, const char* lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Waits until at most N of this wave's copies are outstanding (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_copies_but() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }

@@ -19,6 +19,8 @@
 // MFMA blocks. In a 32x32 block, lane l supplies row l % 32 of A (and of W) at k offset
 // 16 * (l / 32) within each 32-wide k step, and receives C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32]
 // in accumulator register r.
+#include <type_traits>
+
 #include "common.h"
 
 enum Epi { PER_CHANNEL = 0, GROUP_SCALED = 1, RAW_ACC = 2 };
@@ -26,6 +28,99 @@ enum Epi { PER_CHANNEL = 0, GROUP_SCALED = 1, RAW_ACC = 2 };
 #define BK 64
 #define PITCH 80
 #define GT 256
+
+// Dequantizing epilogue of one wave's (32 FI) x (32 FJ) tile at rows mw.., columns nw..: int32 accumulators
+// (or the fp32 group sums for GROUP_SCALED) -> fp16 C, staged through the wave's LDS area `stage`
+// (32 rows of 64 FJ + 16 bytes) so that every lane stores whole 16-byte row segments; RAW_ACC stores the
+// int32 accumulators themselves.
+template <int FI, int FJ, int EPI>
+__device__ __forceinline__ void epilogue(const i16v (&acc)[FI][FJ], const f16v (&yacc)[EPI == GROUP_SCALED ? FI : 1][EPI == GROUP_SCALED ? FJ : 1],
+                                         char* stage, int lane, int mw, int nw, int M, int N, const float* __restrict__ as,
+                                         const float* __restrict__ ws, const half_t* __restrict__ bias, void* __restrict__ Cout,
+                                         const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
+    constexpr int TN = FJ * 32;
+    if (EPI == RAW_ACC) {
+        int* C = (int*)Cout;
+#pragma unroll
+        for (int i = 0; i < FI; i++)
+#pragma unroll
+            for (int j = 0; j < FJ; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = mw + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const int n = nw + j * 32 + (lane & 31);
+                    if (m < M) C[(size_t)m * N + n] = acc[i][j][r];
+                }
+        return;
+    }
+
+    // fp16 epilogue staged through LDS, 32 rows of the wave's tile at a time, so that each
+    // lane stores whole 16-byte row segments.
+    half_t* C = (half_t*)Cout;
+    constexpr int SP = TN * 2 + 16;  // staging row pitch in bytes
+    float wsv[FJ];
+    half_t bv[FJ];
+#pragma unroll
+    for (int j = 0; j < FJ; j++) {
+        const int n = nw + j * 32 + (lane & 31);
+        wsv[j] = EPI == PER_CHANNEL ? ws[n] : 0.f;
+        bv[j] = bias ? bias[n] : (half_t)0;
+    }
+#pragma unroll
+    for (int i = 0; i < FI; i++) {
+        const int mb = mw + i * 32;
+        f4 asv[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            // Rows 8q + 4 (l / 32) + e, e < 4, of this 32-row block.
+            const int mm = mb + 8 * q + 4 * (lane >> 5);
+            if (mm + 3 < M) asv[q] = *(const f4*)(as + mm);
+            else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) asv[q][e] = mm + e < M ? as[mm + e] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FJ; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float s = asv[r >> 2][r & 3];
+                float y;
+                if (EPI == PER_CHANNEL) {
+                    y = (float)acc[i][j][r] * s * wsv[j];
+                    if (bias) y = y + (float)bv[j];
+                } else {
+                    y = yacc[i][j][r] * s;
+                    if (bias) y = y + (float)bv[j];
+                }
+                const int rr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                *(half_t*)(stage + rr * SP + (j * 32 + (lane & 31)) * 2) = to_half(y);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        constexpr int CPR = TN / 8;  // 16-byte chunks per staged row
+#pragma unroll
+        for (int p = 0; p < 32 * CPR / 64; p++) {
+            const int q = lane + p * 64, rr = q / CPR, cc = q % CPR;
+            const int m = mb + rr, n = nw + cc * 8;
+            h8 y = *(const h8*)(stage + rr * SP + cc * 16);
+            if (m < M) {
+                const size_t at = (size_t)m * N + n;
+                if (R) {
+                    const h8 res = *(const h8*)(R + at), gate = *(const h8*)(G + (size_t)(m / L) * N + n);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
+                }
+                *(h8*)(C + at) = y;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 
 template <int BM, int BN, int WM, int WN, bool W4, int EPI>
 __global__ __launch_bounds__(GT, 1) void gemm_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
@@ -151,86 +246,174 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const int8_t* __restrict__ 
         __syncthreads();
     }
 
-    if (EPI == RAW_ACC) {
-        int* C = (int*)Cout;
-#pragma unroll
-        for (int i = 0; i < FI; i++)
-#pragma unroll
-            for (int j = 0; j < FJ; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int m = m0 + wm * TM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const int n = n0 + wn * TN + j * 32 + (lane & 31);
-                    if (m < M) C[(size_t)m * N + n] = acc[i][j][r];
-                }
-        return;
-    }
+    epilogue<FI, FJ, EPI>(acc, yacc, smem + wave * 32 * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
+}
 
-    // fp16 epilogue staged through LDS, 32 rows of the wave's tile at a time, so that each
-    // lane stores whole 16-byte row segments.
-    half_t* C = (half_t*)Cout;
-    constexpr int SP = TN * 2 + 16;  // staging row pitch in bytes
-    char* stage = smem + wave * 32 * SP;
-    float wsv[FJ];
-    half_t bv[FJ];
-#pragma unroll
-    for (int j = 0; j < FJ; j++) {
-        const int n = n0 + wn * TN + j * 32 + (lane & 31);
-        wsv[j] = EPI == PER_CHANNEL ? ws[n] : 0.f;
-        bv[j] = bias ? bias[n] : (half_t)0;
+// int8 x int8 GEMM with direct global->LDS copies (PER_CHANNEL and RAW_ACC epilogues). A workgroup of
+// four wave64s computes a 256 x BN tile, each wave a 128 x BN/2 quarter of 32x32 blocks (accumulators in
+// AGPRs). K advances in 64-byte slices through GS LDS stages: the copies of slice k + GS - 1 go out while
+// slice k is multiplied. A stage holds the slice's 256 A rows, then its BN W rows, 64 bytes each, with the
+// four 16-byte chunks of row r at chunk ^ ((r >> 2) & 3): the fragment reads of 16 consecutive rows then hit
+// 16 distinct bank groups, and one 1 KiB copy instruction (lane i -> bytes 16 i) fills 16 whole rows.
+//
+// One wave per SIMD, so nothing else hides the issue time of copies and LDS reads: each slice is two 32-wide
+// k steps of 12-16 products, and every copy or fragment read is issued in the shadow of one product
+// (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
+// barrier sits between the two k steps of a slice, so the next slice's first reads start right after it.
+#define GS 4
+template <int BN, int EPI>
+__global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
+                                                      const float* __restrict__ ws, const half_t* __restrict__ bias, void* __restrict__ Cout, int M, int N,
+                                                      int K, const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
+    constexpr int BM = 256, TM = 128, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ;
+    constexpr int STAGE = (BM + BN) * BK;
+    constexpr int AI = BM / 64, BI = BN / 64, NI = AI + BI;  // copy instructions per wave per slice
+    static_assert(BN % 64 == 0 && TN % 32 == 0 && NI + FI + FJ <= 2 * NF, "tile");
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave >> 1, wn = wave & 1;
+
+    // Tile order: block ids go round-robin to the 8 XCDs. When the grid allows it, XCD x gets the tiles of
+    // one (gy / 2) x (gx / 4) sub-grid, so each A row panel is read by 4 XCDs' L2s and each W panel by 2
+    // (round-robin order has every XCD read every A panel).
+    int bx = blockIdx.x, by = blockIdx.y;
+    {
+        const int gx = gridDim.x, gy = gridDim.y;
+        if (gx % 4 == 0 && gy % 2 == 0) {
+            const int id = by * gx + bx, x = id % 8, r = id / 8, sx = gx / 4, sy = gy / 2;
+            bx = (x % 4) * sx + r % sx;
+            by = (x / 4) * sy + r / sx;
+        }
     }
+    const int m0 = by * BM, n0 = bx * BN;
+
+    // Copy instruction j of a wave fills the 16 rows 64 j + 16 wave .. of A (or W): lane i takes row
+    // 64 j + crow at physical chunk i % 4, i.e. logical chunk cchunk. A rows past M re-read row M - 1
+    // (their results are not stored); the clamp is folded into the per-lane offsets.
+    const int crow = 16 * wave + (lane >> 2), cchunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const u32 coff = (u32)crow * K + cchunk * 16;
+    // Group c copies from row base arow[c] = min(m0 + 64 c, M - 1); lane offsets are taken from that clamped
+    // base, so they are never negative (the unsigned 32-bit voffset of the copy).
+    int arow[AI];
+    u32 aoff[AI];
 #pragma unroll
-    for (int i = 0; i < FI; i++) {
-        const int mb = m0 + wm * TM + i * 32;
-        f4 asv[4];
+    for (int c = 0; c < AI; c++) {
+        arow[c] = min(m0 + 64 * c, M - 1);
+        aoff[c] = (u32)(min(m0 + 64 * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
+    }
+    auto stage = [&](int kt) -> const char* { return smem + (kt % GS) * STAGE; };
+    auto copy = [&](int kt, int c) {  // copy instruction c (< NI) of slice kt
+        const char* st = stage(kt);
+        const int k0 = kt * BK;
+        if (c < AI) dma16(A + (size_t)arow[c] * K + k0, aoff[c], st + (4 * c + wave) * 1024);
+        else dma16(W + (size_t)(n0 + 64 * (c - AI)) * K + k0, coff, st + BM * BK + (4 * (c - AI) + wave) * 1024);
+    };
+
+    // Fragment f (< FI: A block f, else W block f - FI) of k step kk of a slice: row base + lq, chunk 2 kk + g.
+    const int fx = (lq >> 2) & 3;
+    const u32 foff[2] = {(u32)(lq * BK + ((g ^ fx) << 4)), (u32)(lq * BK + (((2 + g) ^ fx) << 4))};
+    auto frag = [&](const char* st, int kk, int f) -> i4v {
+        return f < FI ? *(const i4v*)(st + (wm * TM + f * 32) * BK + foff[kk]) : *(const i4v*)(st + BM * BK + (wn * TN + (f - FI) * 32) * BK + foff[kk]);
+    };
+    i16v acc[FI][FJ];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            // Rows 8q + 4 (l / 32) + e, e < 4, of this 32-row block.
-            const int mm = mb + 8 * q + 4 * (lane >> 5);
-            if (mm + 3 < M) asv[q] = *(const f4*)(as + mm);
-            else {
+    for (int i = 0; i < FI; i++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) asv[q][e] = mm + e < M ? as[mm + e] : 0.f;
-            }
+        for (int j = 0; j < FJ; j++) acc[i][j] = (i16v){};
+    i4v fr[2][FI + FJ];  // fragments of the current and the next k step
+
+    const int KT = K / BK;
+#pragma unroll
+    for (int kt = 0; kt < GS - 1; kt++)
+        if (kt < KT)
+#pragma unroll
+            for (int c = 0; c < NI; c++) copy(kt, c);
+    // Slice 0 must have landed; up to GS - 2 later slices may still be in flight.
+    if (KT >= GS - 1) wait_copies_but<(GS - 2) * NI>();
+    else wait_copies();
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < FI + FJ; f++) fr[0][f] = frag(stage(0), 0, f);
+
+    // One slice. AHEAD: slice kt + GS - 1 exists and is copied now (into the stage of slice kt - 1, whose
+    // reads ended before the last barrier); MORE: slice kt + 1 exists.
+    auto slice = [&](int kt, auto ahead, auto more) {
+        constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
+        const char* st = stage(kt);
+        // k step 0: product p also issues copy p and then reads fragment p of k step 1.
+#pragma unroll
+        for (int p = 0; p < NF; p++) {
+            acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[0][p / FJ], fr[0][FI + p % FJ], acc[p / FJ][p % FJ], 0, 0, 0);
+            if (AHEAD && p < NI) copy(kt + GS - 1, p);
+            if (p < FI + FJ) fr[1][p] = frag(st, 1, p);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        // Slice kt + 1 has landed once at most GS - 2 slices' copies are outstanding.
+        if (AHEAD) wait_copies_but<(GS - 2) * NI>();
+        else wait_copies();
+        __syncthreads();
+        // k step 1: product p also reads fragment p of the next slice's k step 0.
+        const char* sn = stage(kt + 1);
 #pragma unroll
-        for (int j = 0; j < FJ; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float s = asv[r >> 2][r & 3];
-                float y;
-                if (EPI == PER_CHANNEL) {
-                    y = (float)acc[i][j][r] * s * wsv[j];
-                    if (bias) y = y + (float)bv[j];
-                } else {
-                    y = yacc[i][j][r] * s;
-                    if (bias) y = y + (float)bv[j];
-                }
-                const int rr = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                *(half_t*)(stage + rr * SP + (j * 32 + (lane & 31)) * 2) = to_half(y);
-            }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        constexpr int CPR = TN / 8;  // 16-byte chunks per staged row
-#pragma unroll
-        for (int p = 0; p < 32 * CPR / 64; p++) {
-            const int q = lane + p * 64, rr = q / CPR, cc = q % CPR;
-            const int m = mb + rr, n = n0 + wn * TN + cc * 8;
-            h8 y = *(const h8*)(stage + rr * SP + cc * 16);
-            if (m < M) {
-                const size_t at = (size_t)m * N + n;
-                if (R) {
-                    const h8 res = *(const h8*)(R + at), gate = *(const h8*)(G + (size_t)(m / L) * N + n);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
-                }
-                *(h8*)(C + at) = y;
-            }
+        for (int p = 0; p < NF; p++) {
+            acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[1][p / FJ], fr[1][FI + p % FJ], acc[p / FJ][p % FJ], 0, 0, 0);
+            if (MORE && p < FI + FJ) fr[0][p] = frag(sn, 0, p);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    using yes = std::integral_constant<bool, true>;
+    using no = std::integral_constant<bool, false>;
+    int kt = 0;
+    for (; kt + GS - 1 < KT; kt++) slice(kt, yes{}, yes{});
+    for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{});
+    slice(kt, no{}, no{});
+    __syncthreads();  // the epilogue's staging areas overlap the stages
+    const f16v yacc[1][1] = {};
+    epilogue<FI, FJ, EPI>(acc, yacc, smem + wave * 32 * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
+}
+
+template <int BN, int EPI>
+static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
+                        const void* G, int L, void* stream) {
+    const size_t lds = (size_t)GS * (256 + BN) * BK;
+    auto kern = gemm8_kernel<BN, EPI>;
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return (int)e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(N / BN, (M + 255) / 256), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
+                       (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
+    return (int)hipGetLastError();
+}
+
+// Tile width for the direct-copy kernel: the one of 256, 192, 128 that divides N and leaves the fewest idle
+// CU slots in the last round of 256-CU waves (ties to the wider tile); 0 if none divides N.
+static int gemm8_width(int M, int N) {
+    int best = 0;
+    double best_util = 0.0;
+    for (int bn : {256, 192, 128}) {
+        if (N % bn != 0) continue;
+        const long tiles = (long)((M + 255) / 256) * (N / bn);
+        const double util = (double)tiles / (double)(((tiles + 255) / 256) * 256);
+        if (util > best_util + 1e-9) {
+            best = bn;
+            best_util = util;
+        }
+    }
+    return best;
+}
+
+template <int EPI>
+static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
+                     const void* G, int L, void* stream) {
+    if (K >= (1 << 24)) return -1;  // per-lane copy offsets (< 64 K) must fit the 32-bit voffset
+    switch (gemm8_width(M, N)) {
+        case 256: return launch_gemm8<256, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 192: return launch_gemm8<192, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 128: return launch_gemm8<128, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        default: return -1;
     }
 }
 
@@ -255,6 +438,10 @@ static int dispatch(const void* a, const void* w, const float* as, const float* 
                     int group, const void* R, const void* G, int L, void* stream) {
     if (M <= 0 || N <= 0 || K <= 0 || N % 64 != 0 || K % BK != 0) return RDA_ERR_INVALID;
     if (R && (!G || L <= 0)) return RDA_ERR_INVALID;
+    if constexpr (!W4 && EPI != GROUP_SCALED) {
+        const int e = dispatch8<EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        if (e >= 0) return e;
+    }
     if constexpr (EPI == GROUP_SCALED) {
         if (group <= 0 || group % BK != 0 || K % group != 0) return RDA_ERR_INVALID;
         if (N % 256 == 0) return launch_gemm<128, 256, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
