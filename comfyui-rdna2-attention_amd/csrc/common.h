@@ -94,6 +94,40 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ i4v as_i4(u4v v) { return __builtin_bit_cast(i4v, v); }
 
+// Cross-lane reductions on DPP and lane-swap instructions (one VALU op per step, no LDS round trip).
+// Every lane of a group receives the same bits: partners always add the same two partial values.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) { return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false)); }
+// Over the 16 lanes of each row (lanes 16 r .. 16 r + 15): xor 1, xor 2 (quad_perm), then the half-row
+// mirror (i <-> 7 - i) and the row mirror (i <-> 15 - i).
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
+    return x;
+}
+__device__ __forceinline__ float row_max16(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    x = fmaxf(x, dpp<0x141>(x));
+    x = fmaxf(x, dpp<0x140>(x));
+    return x;
+}
+// Over the four rows (lanes l, l ^ 16, l ^ 32, l ^ 48).
+__device__ __forceinline__ float rows_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float rows_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Direct global->LDS copies: 16 (4) bytes per lane from base + off (or from src), lane i writing LDS

@@ -34,59 +34,69 @@ __global__ __launch_bounds__(256) void rotate_kernel(const float* __restrict__ x
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 
 // out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns RW rows
-// and walks them together in steps of 1024 values (16 per lane; a last half step of 512 when
-// K % 1024 == 512), so one LDS read of x feeds RW rows. x is fp32 or fp16; out has the dtype of x.
-// x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses:
-// the f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
+// and reads them in steps of 1024 values (16 per lane; a last half step of 512 when K % 1024 == 512).
+// All of a wave's weight loads -- at most 16 steps x rows, 16 KiB -- are issued first, before x is
+// staged, so a launch costs one memory round trip rather than one per step; the host picks RW so
+// that the loads fit (RW steps <= 16). x is fp32 or fp16; out has the dtype of x. x sits in LDS in
+// reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the f4 j of lane l
+// in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
 template <int RW, bool XH>
 __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
                                                                  const float* __restrict__ bias, void* __restrict__ out, int N, int K) {
+    constexpr int G = 16 / RW;  // steps whose loads are in flight together
     extern __shared__ f4 xs[];
     const int steps = K / 1024;
-    for (int i = threadIdx.x; i < K / 4; i += GV_WAVES * 64) {
-        f4 v;
-        if (XH) {
-            const h4v hv = ((const h4v*)xin)[i];
-            v = (f4){(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
-        } else {
-            v = ((const f4*)xin)[i];
-        }
-        const int tail = i - steps * 256;
-        xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = v;
-    }
-    __syncthreads();
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = (blockIdx.x * GV_WAVES + wave) * RW;
-    if (row >= N) return;
-    const int8_t* base = w + (size_t)row * K;
+    const bool active = row < N;
+    const int8_t* base = w + (size_t)(active ? row : 0) * K;
+    u4v v[G][RW];
+    u2v vt[RW];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        if (g < steps)
+#pragma unroll
+            for (int r = 0; r < RW; r++) v[g][r] = __builtin_nontemporal_load((const u4v*)(base + (size_t)r * K + g * 1024 + lane * 16));
+    if (K % 1024)
+#pragma unroll
+        for (int r = 0; r < RW; r++) vt[r] = __builtin_nontemporal_load((const u2v*)(base + (size_t)r * K + steps * 1024 + lane * 8));
+
+    for (int i = threadIdx.x; i < K / 4; i += GV_WAVES * 64) {
+        f4 x;
+        if (XH) {
+            const h4v hv = ((const h4v*)xin)[i];
+            x = (f4){(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
+        } else {
+            x = ((const f4*)xin)[i];
+        }
+        const int tail = i - steps * 256;
+        xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = x;
+    }
+    __syncthreads();
+    if (!active) return;
     float acc[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) acc[r] = 0.f;
-    for (int s = 0; s < steps; s++) {
-        u4v v[RW];
 #pragma unroll
-        for (int r = 0; r < RW; r++) v[r] = __builtin_nontemporal_load((const u4v*)(base + (size_t)r * K + s * 1024 + lane * 16));
+    for (int g = 0; g < G; g++) {
+        if (g >= steps) continue;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const f4 xv = xs[(s * 4 + j) * 64 + lane];
+            const f4 xv = xs[(g * 4 + j) * 64 + lane];
 #pragma unroll
             for (int r = 0; r < RW; r++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[r][j], i), xv[i], acc[r]);
+                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[g][r][j], i), xv[i], acc[r]);
         }
     }
     if (K % 1024) {
-        const int k0 = steps * 1024 + lane * 8;
-        u2v v[RW];
-#pragma unroll
-        for (int r = 0; r < RW; r++) v[r] = __builtin_nontemporal_load((const u2v*)(base + (size_t)r * K + k0));
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const f4 xv = xs[steps * 256 + j * 64 + lane];
 #pragma unroll
             for (int r = 0; r < RW; r++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[r][j], i), xv[i], acc[r]);
+                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(vt[r][j], i), xv[i], acc[r]);
         }
     }
 #pragma unroll
@@ -154,48 +164,91 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_bf16_kernel(const float* _
 
 // attn_decode (int8_gemv.hip:121-180): one new token over the cache, split by position so that a few
 // KV heads still fill the GPU. The grid is fixed and the length is read here, so a captured graph
-// stays valid as the cache grows. A wave takes one position at a time: a K or V row of a head is
-// 512 bytes, 8 per lane, shared by the REP query heads of the KV head.
+// stays valid as the cache grows. Memory-level parallelism is the point: a wave takes 16 positions at
+// once (16 lanes per position, 8 dims per lane), issues all their K and V loads before any arithmetic,
+// then folds the 16 scores of each query head into its running (max, sum, acc) with one rescale. The
+// REP query heads of the KV head share every load.
 template <int REP>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
                                                           const int* __restrict__ lengths, float* __restrict__ partial, float* __restrict__ stats,
                                                           int capacity, int kv_heads, float scale) {
-    constexpr int W = 4;
+    constexpr int W = 4, ITS = 4, PW = 4 * ITS;  // waves; 4-position steps per round; positions per wave per round
     __shared__ float acc_s[W][REP][HEAD];
     __shared__ float max_s[W][REP], sum_s[W][REP];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, pos = lane >> 4, sub = lane & 15;
     const int b = blockIdx.y / kv_heads, kv_head = blockIdx.y % kv_heads, split = blockIdx.x;
     const int length = lengths[b];
     const int chunk = (length + SPLITS - 1) / SPLITS;
-    const int end = min((split + 1) * chunk, length);
+    const int begin = split * chunk, end = min(begin + chunk, length);
     const int first_head = (b * kv_heads + kv_head) * REP;
 
-    f2 qv[REP], acc[REP];
+    f4 qv[REP][2], acc[REP][2];
     float mx[REP], sum[REP];
 #pragma unroll
     for (int g = 0; g < REP; g++) {
-        qv[g] = ((const f2*)(q + (size_t)(first_head + g) * HEAD))[lane] * scale;
-        acc[g] = (f2){0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            qv[g][h] = ((const f4*)(q + (size_t)(first_head + g) * HEAD + sub * 8))[h] * scale;
+            acc[g][h] = (f4){0.f, 0.f, 0.f, 0.f};
+        }
         mx[g] = -1e30f;
         sum[g] = 0.f;
     }
-    for (int j = split * chunk + wave; j < end; j += W) {
-        const size_t row = ((size_t)(b * capacity + j) * kv_heads + kv_head) * HEAD;
-        const f2 kv = ((const f2*)(k + row))[lane], vv = ((const f2*)(v + row))[lane];
+    for (int base = begin + wave * PW; base < end; base += W * PW) {
+        f4 kr[ITS][2], vr[ITS][2];
+        bool valid[ITS];
+#pragma unroll
+        for (int it = 0; it < ITS; it++) {
+            const int j = base + it * 4 + pos;
+            valid[it] = j < end;
+            const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
+            kr[it][0] = *(const f4*)(k + row);
+            kr[it][1] = *(const f4*)(k + row + 4);
+            vr[it][0] = *(const f4*)(v + row);
+            vr[it][1] = *(const f4*)(v + row + 4);
+        }
 #pragma unroll
         for (int g = 0; g < REP; g++) {
-            const f2 d = qv[g] * kv;
-            const float score = wave_sum(d[0] + d[1]);
-            const float next = fmaxf(mx[g], score);
-            const float keep = expf(mx[g] - next), p = expf(score - next);
-            sum[g] = sum[g] * keep + p;
-            acc[g] = acc[g] * keep + vv * p;
+            float s[ITS];
+            float top = -1e30f;
+#pragma unroll
+            for (int it = 0; it < ITS; it++) {
+                const f4 d = qv[g][0] * kr[it][0] + qv[g][1] * kr[it][1];
+                const float x = row_sum16((d[0] + d[1]) + (d[2] + d[3]));
+                s[it] = valid[it] ? x : -1e30f;
+                top = fmaxf(top, s[it]);
+            }
+            top = rows_max(top);
+            const float next = fmaxf(mx[g], top), keep = __expf(mx[g] - next);
+            float psum = 0.f;
+            f4 a0 = acc[g][0] * keep, a1 = acc[g][1] * keep;
+#pragma unroll
+            for (int it = 0; it < ITS; it++) {
+                const float p = valid[it] ? __expf(s[it] - next) : 0.f;
+                psum += p;
+                a0 += vr[it][0] * p;
+                a1 += vr[it][1] * p;
+            }
+            psum = rows_sum(psum);
+            sum[g] = sum[g] * keep + psum;
+            acc[g][0] = a0;
+            acc[g][1] = a1;
             mx[g] = next;
         }
     }
+    // The four position groups of the wave hold partial sums of the same dims: add them up.
+#pragma unroll
+    for (int g = 0; g < REP; g++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[g][h][e] = rows_sum(acc[g][h][e]);
 #pragma unroll
     for (int g = 0; g < REP; g++) {
-        ((f2*)acc_s[wave][g])[lane] = acc[g];
+        if (pos == 0) {
+            ((f4*)acc_s[wave][g])[sub * 2] = acc[g][0];
+            ((f4*)acc_s[wave][g])[sub * 2 + 1] = acc[g][1];
+        }
         if (lane == 0) {
             max_s[wave][g] = mx[g];
             sum_s[wave][g] = sum[g];
@@ -210,7 +263,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         float value = 0.f, total = 0.f;
 #pragma unroll
         for (int w = 0; w < W; w++) {
-            const float keep = expf(max_s[w][g] - top);
+            const float keep = __expf(max_s[w][g] - top);
             value += acc_s[w][g][d] * keep;
             total += sum_s[w][g] * keep;
         }
@@ -231,7 +284,7 @@ __global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restric
     for (int s = 1; s < SPLITS; s++) top = fmaxf(top, st[s * 2]);
     float value = 0.f, total = 0.f;
     for (int s = 0; s < SPLITS; s++) {
-        const float keep = expf(st[s * 2] - top);
+        const float keep = __expf(st[s * 2] - top);
         value += partial[(head * SPLITS + s) * HEAD + threadIdx.x] * keep;
         total += st[s * 2 + 1] * keep;
     }
@@ -257,10 +310,18 @@ int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
 // x_half: 0 for fp32 x and out, 1 for fp16 x and out.
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
     if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384 || N % 4 != 0) return RDA_ERR_INVALID;
-    // Enough rows per wave to amortise the x staging, few enough that every CU gets work.
-    const bool many = N >= 4096 && N % (GV_WAVES * 4) == 0;
-    if (x_half) return many ? launch_gemv<4, true>(x, w, scale, bias, out, N, K, stream) : launch_gemv<1, true>(x, w, scale, bias, out, N, K, stream);
-    return many ? launch_gemv<4, false>(x, w, scale, bias, out, N, K, stream) : launch_gemv<1, false>(x, w, scale, bias, out, N, K, stream);
+    // Rows per wave: as many as keep the wave's loads within 16 steps and the grid at >= 256 workgroups.
+    const int steps = (K + 1023) / 1024;
+    int rw = steps <= 4 ? 4 : steps <= 8 ? 2 : 1;
+    while (rw > 1 && (N % (GV_WAVES * rw) != 0 || N / (GV_WAVES * rw) < 256)) rw /= 2;
+    switch (rw * 2 + (x_half ? 1 : 0)) {
+    case 8: return launch_gemv<4, false>(x, w, scale, bias, out, N, K, stream);
+    case 9: return launch_gemv<4, true>(x, w, scale, bias, out, N, K, stream);
+    case 4: return launch_gemv<2, false>(x, w, scale, bias, out, N, K, stream);
+    case 5: return launch_gemv<2, true>(x, w, scale, bias, out, N, K, stream);
+    case 2: return launch_gemv<1, false>(x, w, scale, bias, out, N, K, stream);
+    default: return launch_gemv<1, true>(x, w, scale, bias, out, N, K, stream);
+    }
 }
 
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream) {
