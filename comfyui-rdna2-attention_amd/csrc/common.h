@@ -27,7 +27,7 @@ typedef u32 u4v __attribute__((ext_vector_type(4)));
 // folds a preceding fp32 multiply or FMA into v_fma_mixlo_f16, which rounds the exact product once, straight to
 // fp16; every rounding point in these kernels is "round to fp32, then to fp16", as the arithmetic is written.
 __device__ __forceinline__ half_t to_half(float x) {
-    asm volatile("" : "+v"(x));
+    asm("" : "+v"(x));  // not volatile: the scheduler may still interleave independent conversions
     return (half_t)x;
 }
 // Rounds an fp32 value to fp16 and back.

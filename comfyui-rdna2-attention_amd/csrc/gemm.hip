@@ -249,26 +249,132 @@ __global__ __launch_bounds__(GT, 1) void gemm_kernel(const int8_t* __restrict__ 
     epilogue<FI, FJ, EPI>(acc, yacc, smem + wave * 32 * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
 }
 
+// Epilogue for accumulators holding C^T blocks (the GEMM computed W A^T): in block (i, j), lane l owns
+// row mw + 32 i + l % 32 of C and register r holds column nw + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4, so
+// each group of four registers is four consecutive columns of one row: they are dequantized and stored
+// as 8-byte fp16 (16-byte int32) row segments, with no staging.
+template <int FI, int FJ, int EPI>
+__device__ __forceinline__ void epilogue_rows(const i16v (&acc)[FI][FJ], int lane, int mw, int nw, int M, int N, const float* __restrict__ as,
+                                              const float* __restrict__ ws, const half_t* __restrict__ bias, void* __restrict__ Cout,
+                                              const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
+    const int lq = lane & 31, g = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FI; i++) {
+        const int m = mw + i * 32 + lq;
+        if (m >= M) continue;
+        const float s = EPI == RAW_ACC ? 0.f : as[m];
+#pragma unroll
+        for (int j = 0; j < FJ; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int n = nw + j * 32 + 8 * q + 4 * g;
+                const size_t at = (size_t)m * N + n;
+                if (EPI == RAW_ACC) {
+                    *(i4v*)((int*)Cout + at) = (i4v){acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    continue;
+                }
+                const f4 wv = *(const f4*)(ws + n);
+                h4v bv = {};
+                if (bias) bv = *(const h4v*)(bias + n);
+                h4v y;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float v = (float)acc[i][j][4 * q + e] * s * wv[e];
+                    if (bias) v = v + (float)bv[e];
+                    y[e] = to_half(v);
+                }
+                if (R) {
+                    const h4v res = *(const h4v*)(R + at), gate = *(const h4v*)(G + (size_t)(m / L) * N + n);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
+                }
+                *(h4v*)((half_t*)Cout + at) = y;
+            }
+    }
+}
+
+// Epilogue of the whole 256 x BN block through LDS: every wave dequantizes its C^T accumulators (scales
+// and biases from the scale block `sc` in LDS)
+// (epilogue_rows' register layout) into an fp16 tile in LDS, then all 256 threads store it in 16-byte
+// chunks, consecutive lanes covering consecutive bytes of a row, so each store instruction writes whole
+// 128-byte lines (the register layout would touch 32 rows per instruction). R and G are read the same way.
+// Bytes of the bias area of the scale block: BN halfs, copied in 256-byte instructions.
+constexpr int SC_BIAS(int bn) { return (bn * 2 + 255) / 256 * 256; }
+template <int BN, int FI, int FJ>
+__device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], char* tile, const char* sc, int t, int lane, int wm, int wn, int m0, int n0, int M, int N,
+                                               const float* __restrict__ as, const float* __restrict__ ws, const half_t* __restrict__ bias,
+                                               half_t* __restrict__ C, const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
+    constexpr int TM = FI * 32, TN = FJ * 32, TP = BN * 2 + 16, CPR = BN / 8;  // tile row pitch (bytes), 16-byte chunks per row
+    const int lq = lane & 31, g = lane >> 5;
+    // The block's column scales, biases and row scales were copied into LDS at the kernel's start.
+    const float* ws_s = (const float*)sc;
+    const half_t* bias_s = (const half_t*)(sc + BN * 4);
+    const float* as_s = (const float*)(sc + BN * 4 + SC_BIAS(BN));
+    auto dequantize = [&](auto has_bias) {
+        constexpr bool HB = decltype(has_bias)::value;
+#pragma unroll
+        for (int j = 0; j < FJ; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int c = wn * TN + j * 32 + 8 * q + 4 * g;
+                const f4 wv = *(const f4*)(ws_s + c);
+                const h4v bv = HB ? *(const h4v*)(bias_s + c) : (h4v){};
+#pragma unroll
+                for (int i = 0; i < FI; i++) {
+                    const int r = wm * TM + i * 32 + lq;
+                    const float sv = as_s[r];
+                    h4v y;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        float v = (float)acc[i][j][4 * q + e] * sv * wv[e];
+                        if (HB) v = v + (float)bv[e];
+                        y[e] = to_half(v);
+                    }
+                    *(h4v*)(tile + r * TP + c * 2) = y;
+                }
+            }
+    };
+    if (bias) dequantize(std::integral_constant<bool, true>{});
+    else dequantize(std::integral_constant<bool, false>{});
+    __syncthreads();
+#pragma unroll 4
+    for (int idx = t; idx < 256 * CPR; idx += GT) {
+        const int r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
+        if (m >= M) continue;
+        h8 y = *(const h8*)(tile + r * TP + c * 2);
+        const size_t at = (size_t)m * N + n0 + c;
+        if (R) {
+            const h8 res = *(const h8*)(R + at), gate = *(const h8*)(G + (size_t)(m / L) * N + n0 + c);
+#pragma unroll
+            for (int e = 0; e < 8; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
+        }
+        *(h8*)(C + at) = y;
+    }
+}
+
 // int8 x int8 GEMM with direct global->LDS copies (PER_CHANNEL and RAW_ACC epilogues). A workgroup of
 // four wave64s computes a 256 x BN tile, each wave a 128 x BN/2 quarter of 32x32 blocks (accumulators in
-// AGPRs). K advances in 64-byte slices through GS LDS stages: the copies of slice k + GS - 1 go out while
-// slice k is multiplied. A stage holds the slice's 256 A rows, then its BN W rows, 64 bytes each, with the
-// four 16-byte chunks of row r at chunk ^ ((r >> 2) & 3): the fragment reads of 16 consecutive rows then hit
-// 16 distinct bank groups, and one 1 KiB copy instruction (lane i -> bytes 16 i) fills 16 whole rows.
+// AGPRs; the products compute W A^T, so each lane ends up owning row segments of C). K advances in
+// slices of KB8 bytes through NS LDS stages: the copies of slice k + NS - 1 go out while slice k is
+// multiplied. A stage holds the slice's 256 A rows, then its BN W rows, KB8 bytes each, with 16-byte chunk
+// c of row r at c ^ ((r / RPL) % CPR) (RPL rows per 256-byte bank line, CPR chunks per row): the fragment
+// reads of 16 consecutive rows then hit 16 distinct bank groups, and one 1 KiB copy instruction (lane i ->
+// bytes 16 i) fills 1024 / KB8 whole rows.
 //
-// One wave per SIMD, so nothing else hides the issue time of copies and LDS reads: each slice is two 32-wide
-// k steps of 12-16 products, and every copy or fragment read is issued in the shadow of one product
+// One wave per SIMD, so nothing else hides the issue time of copies and LDS reads: every copy and
+// fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
-// barrier sits between the two k steps of a slice, so the next slice's first reads start right after it.
-#define GS 4
-template <int BN, int EPI>
+// slice's barrier sits before its last k step, so the next slice's first reads start right after it.
+template <int BN, int KB8, int NS, int EPI>
 __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
                                                       const float* __restrict__ ws, const half_t* __restrict__ bias, void* __restrict__ Cout, int M, int N,
                                                       int K, const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
-    constexpr int BM = 256, TM = 128, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ;
-    constexpr int STAGE = (BM + BN) * BK;
-    constexpr int AI = BM / 64, BI = BN / 64, NI = AI + BI;  // copy instructions per wave per slice
-    static_assert(BN % 64 == 0 && TN % 32 == 0 && NI + FI + FJ <= 2 * NF, "tile");
+    constexpr int BM = 256, TM = 128, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
+    constexpr int KS = KB8 / 32;                                   // 32-wide k steps per slice
+    constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // chunks per row, rows per copy, rows per bank line
+    constexpr int STAGE = (BM + BN) * KB8;
+    constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPI), NI = AI + BI;  // copy instructions per wave per slice
+    static_assert(BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPI) == 0, "tile");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave >> 1, wn = wave & 1;
@@ -287,96 +393,134 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
     }
     const int m0 = by * BM, n0 = bx * BN;
 
-    // Copy instruction j of a wave fills the 16 rows 64 j + 16 wave .. of A (or W): lane i takes row
-    // 64 j + crow at physical chunk i % 4, i.e. logical chunk cchunk. A rows past M re-read row M - 1
-    // (their results are not stored); the clamp is folded into the per-lane offsets.
-    const int crow = 16 * wave + (lane >> 2), cchunk = (lane & 3) ^ ((lane >> 4) & 3);
+    // Copy instruction j of a wave fills rows (4 j + wave) RPI .. + RPI - 1 of A (or W): lane i takes row
+    // (4 j + wave) RPI + i / CPR at physical chunk i % CPR, i.e. logical chunk cchunk (the swizzle term is the
+    // same for every j). A rows past M re-read row M - 1 (their results are not stored); the clamp is folded
+    // into the per-lane offsets, taken from a clamped group base so that they are never negative (they are
+    // the unsigned 32-bit voffset of the copy).
+    const int crow = wave * RPI + lane / CPR;
+    const int cchunk = (lane % CPR) ^ ((crow / RPL) % CPR);
     const u32 coff = (u32)crow * K + cchunk * 16;
-    // Group c copies from row base arow[c] = min(m0 + 64 c, M - 1); lane offsets are taken from that clamped
-    // base, so they are never negative (the unsigned 32-bit voffset of the copy).
     int arow[AI];
     u32 aoff[AI];
 #pragma unroll
     for (int c = 0; c < AI; c++) {
-        arow[c] = min(m0 + 64 * c, M - 1);
-        aoff[c] = (u32)(min(m0 + 64 * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
+        arow[c] = min(m0 + 4 * RPI * c, M - 1);
+        aoff[c] = (u32)(min(m0 + 4 * RPI * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
     }
-    auto stage = [&](int kt) -> const char* { return smem + (kt % GS) * STAGE; };
+    auto stage = [&](int kt) -> const char* { return smem + (kt % NS) * STAGE; };
+    // The epilogue's scales go to a scale block past the stages and the staged tile: ws[n0 .. n0 + BN) (BN / 64
+    // copies of 64 floats), bias[n0 ..) (256-byte copies, lanes past BN / 2 re-read the last pair) and
+    // as[m0 .. m0 + 256) (rows past M re-read row M - 1), each copy issued by one wave.
+    constexpr int SC_OFF = ((NS * STAGE > 256 * (BN * 2 + 16) ? NS * STAGE : 256 * (BN * 2 + 16)) + 255) / 256 * 256;
+    const char* sc = smem + SC_OFF;
+    if (EPI != RAW_ACC) {
+        constexpr int NWS = BN / 64, NB = SC_BIAS(BN) / 256;
+#pragma unroll
+        for (int c = 0; c < NWS + NB + 4; c++) {
+            if (c % 4 != wave) continue;
+            if (c < NWS) {
+                dma4(ws + n0 + 64 * c, lane * 4, sc + c * 256);
+            } else if (c < NWS + NB) {
+                if (bias) dma4(bias + n0, (u32)min(64 * (c - NWS) + lane, BN / 2 - 1) * 4, sc + BN * 4 + (c - NWS) * 256);
+            } else {
+                const int i = c - NWS - NB, mb = min(m0 + 64 * i, M - 1);
+                dma4(as + mb, (u32)(min(m0 + 64 * i + lane, M - 1) - mb) * 4, sc + BN * 4 + SC_BIAS(BN) + i * 256);
+            }
+        }
+    }
     auto copy = [&](int kt, int c) {  // copy instruction c (< NI) of slice kt
         const char* st = stage(kt);
-        const int k0 = kt * BK;
+        const int k0 = kt * KB8;
         if (c < AI) dma16(A + (size_t)arow[c] * K + k0, aoff[c], st + (4 * c + wave) * 1024);
-        else dma16(W + (size_t)(n0 + 64 * (c - AI)) * K + k0, coff, st + BM * BK + (4 * (c - AI) + wave) * 1024);
+        else dma16(W + (size_t)(n0 + 4 * RPI * (c - AI)) * K + k0, coff, st + BM * KB8 + (4 * (c - AI) + wave) * 1024);
     };
 
-    // Fragment f (< FI: A block f, else W block f - FI) of k step kk of a slice: row base + lq, chunk 2 kk + g.
-    const int fx = (lq >> 2) & 3;
-    const u32 foff[2] = {(u32)(lq * BK + ((g ^ fx) << 4)), (u32)(lq * BK + (((2 + g) ^ fx) << 4))};
+    // Fragment f (< FI: A block f, else W block f - FI) of k step kk: row base + lq, chunk 2 kk + g.
+    const int fx = (lq / RPL) % CPR;
     auto frag = [&](const char* st, int kk, int f) -> i4v {
-        return f < FI ? *(const i4v*)(st + (wm * TM + f * 32) * BK + foff[kk]) : *(const i4v*)(st + BM * BK + (wn * TN + (f - FI) * 32) * BK + foff[kk]);
+        const u32 off = (u32)(lq * KB8 + (((2 * kk + g) ^ fx) << 4));
+        return f < FI ? *(const i4v*)(st + (wm * TM + f * 32) * KB8 + off) : *(const i4v*)(st + BM * KB8 + (wn * TN + (f - FI) * 32) * KB8 + off);
     };
     i16v acc[FI][FJ];
 #pragma unroll
     for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++) acc[i][j] = (i16v){};
-    i4v fr[2][FI + FJ];  // fragments of the current and the next k step
+    i4v fr[2][NR];  // fragments of the current and the next k step
 
-    const int KT = K / BK;
+    const int KT = K / KB8;
 #pragma unroll
-    for (int kt = 0; kt < GS - 1; kt++)
+    for (int kt = 0; kt < NS - 1; kt++)
         if (kt < KT)
 #pragma unroll
             for (int c = 0; c < NI; c++) copy(kt, c);
-    // Slice 0 must have landed; up to GS - 2 later slices may still be in flight.
-    if (KT >= GS - 1) wait_copies_but<(GS - 2) * NI>();
+    // Slice 0 must have landed; up to NS - 2 later slices may still be in flight.
+    if (KT >= NS - 1) wait_copies_but<(NS - 2) * NI>();
     else wait_copies();
     __syncthreads();
 #pragma unroll
-    for (int f = 0; f < FI + FJ; f++) fr[0][f] = frag(stage(0), 0, f);
+    for (int f = 0; f < NR; f++) fr[0][f] = frag(stage(0), 0, f);
 
-    // One slice. AHEAD: slice kt + GS - 1 exists and is copied now (into the stage of slice kt - 1, whose
+    // Copies of a slice are spread over its first CKS k steps: k step ks issues copies [CB(ks), CB(ks + 1)).
+    // With two stages the copies of slice k + 1 go out during slice k, so all of them must precede the
+    // barrier that publishes it (before the last k step); with more stages they may follow it.
+    constexpr int CKS = NS == 2 ? KS - 1 : KS;
+    constexpr auto CB = [](int ks) { return (ks < CKS ? ks : CKS) * NI / CKS; };
+    // Copies that may still be in flight at that barrier once slice k + 1 has landed: the NS - 3 slices
+    // after it, and the part of slice k + NS - 1 issued before the barrier.
+    constexpr int LEFT = NS == 2 ? 0 : (NS - 3) * NI + CB(KS - 1);
+    // One slice. AHEAD: slice kt + NS - 1 exists and is copied now (into the stage of slice kt - 1, whose
     // reads ended before the last barrier); MORE: slice kt + 1 exists.
     auto slice = [&](int kt, auto ahead, auto more) {
         constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
         const char* st = stage(kt);
-        // k step 0: product p also issues copy p and then reads fragment p of k step 1.
-#pragma unroll
-        for (int p = 0; p < NF; p++) {
-            acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[0][p / FJ], fr[0][FI + p % FJ], acc[p / FJ][p % FJ], 0, 0, 0);
-            if (AHEAD && p < NI) copy(kt + GS - 1, p);
-            if (p < FI + FJ) fr[1][p] = frag(st, 1, p);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        // Slice kt + 1 has landed once at most GS - 2 slices' copies are outstanding.
-        if (AHEAD) wait_copies_but<(GS - 2) * NI>();
-        else wait_copies();
-        __syncthreads();
-        // k step 1: product p also reads fragment p of the next slice's k step 0.
         const char* sn = stage(kt + 1);
 #pragma unroll
-        for (int p = 0; p < NF; p++) {
-            acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[1][p / FJ], fr[1][FI + p % FJ], acc[p / FJ][p % FJ], 0, 0, 0);
-            if (MORE && p < FI + FJ) fr[0][p] = frag(sn, 0, p);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int ks = 0; ks < KS; ks++) {
+            if (ks == KS - 1) {
+                if (AHEAD) wait_copies_but<LEFT>();  // slice kt + 1 has landed
+                else wait_copies();
+                __syncthreads();
+            }
+            const int cur = ks & 1, nxt = cur ^ 1;
+            const bool last = ks == KS - 1;
+            const int nc = CB(ks + 1) - CB(ks);
+#pragma unroll
+            for (int p = 0; p < NF; p++) {
+                acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[cur][FI + p % FJ], fr[cur][p / FJ], acc[p / FJ][p % FJ], 0, 0, 0);
+                if (AHEAD)
+#pragma unroll
+                    for (int c = 0; c < nc; c++)
+                        if (c * NF / nc == p) copy(kt + NS - 1, CB(ks) + c);
+                if (!last || MORE)
+#pragma unroll
+                    for (int f = 0; f < NR; f++)
+                        if ((f * NF + NF / 2) / NR == p) fr[nxt][f] = last ? frag(sn, 0, f) : frag(st, ks + 1, f);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
     int kt = 0;
-    for (; kt + GS - 1 < KT; kt++) slice(kt, yes{}, yes{});
+    for (; kt + NS - 1 < KT; kt++) slice(kt, yes{}, yes{});
     for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{});
     slice(kt, no{}, no{});
-    __syncthreads();  // the epilogue's staging areas overlap the stages
-    const f16v yacc[1][1] = {};
-    epilogue<FI, FJ, EPI>(acc, yacc, smem + wave * 32 * (TN * 2 + 16), lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
+    if constexpr (EPI == RAW_ACC) {
+        epilogue_rows<FI, FJ, EPI>(acc, lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
+    } else {
+        __syncthreads();  // the staged tile overlaps the stages
+        epilogue_block<BN, FI, FJ>(acc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
+    }
 }
 
-template <int BN, int EPI>
+template <int BN, int KB8, int NS, int EPI>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
                         const void* G, int L, void* stream) {
-    const size_t lds = (size_t)GS * (256 + BN) * BK;
-    auto kern = gemm8_kernel<BN, EPI>;
+    const size_t stages = (size_t)NS * (256 + BN) * KB8, tile = (size_t)256 * (BN * 2 + 16);
+    const size_t lds = EPI == RAW_ACC ? stages : ((stages > tile ? stages : tile) + 255) / 256 * 256 + BN * 4 + SC_BIAS(BN) + 1024;
+    auto kern = gemm8_kernel<BN, KB8, NS, EPI>;
     static bool configured = false;
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -409,10 +553,18 @@ template <int EPI>
 static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
                      const void* G, int L, void* stream) {
     if (K >= (1 << 24)) return -1;  // per-lane copy offsets (< 64 K) must fit the 32-bit voffset
-    switch (gemm8_width(M, N)) {
-        case 256: return launch_gemm8<256, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 192: return launch_gemm8<192, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 128: return launch_gemm8<128, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+    // The row-segment epilogue reads ws as float4 and bias / R / G and writes C as 8-byte (int32: 16-byte) vectors.
+    auto aligned = [](const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; };
+    if (!aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
+    // 128-byte k slices in two stages when K allows, else 64-byte slices in four.
+    const bool wide = K % 128 == 0;
+    switch (gemm8_width(M, N) * 2 + (wide ? 1 : 0)) {
+        case 513: return launch_gemm8<256, 128, 2, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 385: return launch_gemm8<192, 128, 2, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 257: return launch_gemm8<128, 128, 3, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 512: return launch_gemm8<256, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 384: return launch_gemm8<192, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+        case 256: return launch_gemm8<128, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
         default: return -1;
     }
 }
