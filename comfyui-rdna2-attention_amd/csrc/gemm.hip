@@ -409,11 +409,11 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
         aoff[c] = (u32)(min(m0 + 4 * RPI * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
     }
     auto stage = [&](int kt) -> const char* { return smem + (kt % NS) * STAGE; };
-    // The epilogue's scales go to a scale block past the stages and the staged tile: ws[n0 .. n0 + BN) (BN / 64
+    // The epilogue's scales go to a scale block: ws[n0 .. n0 + BN) (BN / 64
     // copies of 64 floats), bias[n0 ..) (256-byte copies, lanes past BN / 2 re-read the last pair) and
     // as[m0 .. m0 + 256) (rows past M re-read row M - 1), each copy issued by one wave.
-    constexpr int SC_OFF = ((NS * STAGE > 256 * (BN * 2 + 16) ? NS * STAGE : 256 * (BN * 2 + 16)) + 255) / 256 * 256;
-    const char* sc = smem + SC_OFF;
+    // (A static LDS array of its own: the compiler can then tell the epilogue's scale reads from its tile writes.)
+    __shared__ __attribute__((aligned(16))) char sc[BN * 4 + SC_BIAS(BN) + 1024];
     if (EPI != RAW_ACC) {
         constexpr int NWS = BN / 64, NB = SC_BIAS(BN) / 256;
 #pragma unroll
@@ -519,7 +519,7 @@ template <int BN, int KB8, int NS, int EPI>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
                         const void* G, int L, void* stream) {
     const size_t stages = (size_t)NS * (256 + BN) * KB8, tile = (size_t)256 * (BN * 2 + 16);
-    const size_t lds = EPI == RAW_ACC ? stages : ((stages > tile ? stages : tile) + 255) / 256 * 256 + BN * 4 + SC_BIAS(BN) + 1024;
+    const size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
     auto kern = gemm8_kernel<BN, KB8, NS, EPI>;
     static bool configured = false;
     if (!configured) {
