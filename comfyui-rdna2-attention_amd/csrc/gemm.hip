@@ -293,15 +293,16 @@ __device__ __forceinline__ void epilogue_rows(const i16v (&acc)[FI][FJ], int lan
     }
 }
 
-// Epilogue of the whole 256 x BN block through LDS: every wave dequantizes its C^T accumulators (scales
-// and biases from the scale block `sc` in LDS)
-// (epilogue_rows' register layout) into an fp16 tile in LDS, then all 256 threads store it in 16-byte
+// Epilogue of the whole 256 x BN block through LDS: every wave dequantizes its C^T accumulators
+// (epilogue_rows' register layout; scales and biases from the scale block `sc` in LDS; GROUP_SCALED: the
+// fp32 group sums yacc, times as) into an fp16 tile in LDS, then all 256 threads store it in 16-byte
 // chunks, consecutive lanes covering consecutive bytes of a row, so each store instruction writes whole
 // 128-byte lines (the register layout would touch 32 rows per instruction). R and G are read the same way.
 // Bytes of the bias area of the scale block: BN halfs, copied in 256-byte instructions.
 constexpr int SC_BIAS(int bn) { return (bn * 2 + 255) / 256 * 256; }
-template <int BN, int FI, int FJ>
-__device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], char* tile, const char* sc, int t, int lane, int wm, int wn, int m0, int n0, int M, int N,
+template <int BN, int FI, int FJ, int EPI>
+__device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const f16v (&yacc)[EPI == GROUP_SCALED ? FI : 1][EPI == GROUP_SCALED ? FJ : 1],
+                                               char* tile, const char* sc, int t, int lane, int wm, int wn, int m0, int n0, int M, int N,
                                                const float* __restrict__ as, const float* __restrict__ ws, const half_t* __restrict__ bias,
                                                half_t* __restrict__ C, const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
     constexpr int TM = FI * 32, TN = FJ * 32, TP = BN * 2 + 16, CPR = BN / 8;  // tile row pitch (bytes), 16-byte chunks per row
@@ -317,7 +318,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], char* 
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int c = wn * TN + j * 32 + 8 * q + 4 * g;
-                const f4 wv = *(const f4*)(ws_s + c);
+                const f4 wv = EPI == PER_CHANNEL ? *(const f4*)(ws_s + c) : (f4){};
                 const h4v bv = HB ? *(const h4v*)(bias_s + c) : (h4v){};
 #pragma unroll
                 for (int i = 0; i < FI; i++) {
@@ -326,7 +327,9 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], char* 
                     h4v y;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        float v = (float)acc[i][j][4 * q + e] * sv * wv[e];
+                        float v;
+                        if constexpr (EPI == PER_CHANNEL) v = (float)acc[i][j][4 * q + e] * sv * wv[e];
+                        else v = yacc[EPI == GROUP_SCALED ? i : 0][EPI == GROUP_SCALED ? j : 0][4 * q + e] * sv;
                         if (HB) v = v + (float)bv[e];
                         y[e] = to_half(v);
                     }
@@ -352,29 +355,40 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], char* 
     }
 }
 
-// int8 x int8 GEMM with direct global->LDS copies (PER_CHANNEL and RAW_ACC epilogues). A workgroup of
-// four wave64s computes a 256 x BN tile, each wave a 128 x BN/2 quarter of 32x32 blocks (accumulators in
-// AGPRs; the products compute W A^T, so each lane ends up owning row segments of C). K advances in
-// slices of KB8 bytes through NS LDS stages: the copies of slice k + NS - 1 go out while slice k is
-// multiplied. A stage holds the slice's 256 A rows, then its BN W rows, KB8 bytes each, with 16-byte chunk
-// c of row r at c ^ ((r / RPL) % CPR) (RPL rows per 256-byte bank line, CPR chunks per row): the fragment
-// reads of 16 consecutive rows then hit 16 distinct bank groups, and one 1 KiB copy instruction (lane i ->
-// bytes 16 i) fills 1024 / KB8 whole rows.
+// int8 GEMM with direct global->LDS copies, for int8 or packed int4 weights (PER_CHANNEL, GROUP_SCALED and
+// RAW_ACC epilogues). A workgroup of four wave64s computes a 256 x BN tile, each wave a 128 x BN/2 quarter
+// of 32x32 blocks (accumulators in AGPRs; the products compute W A^T, so each lane ends up owning row
+// segments of C). K advances in slices of KB8 values through NS LDS stages: the copies of slice k + NS - 1
+// go out while slice k is multiplied. A stage holds the slice's 256 A rows (KB8 bytes each), then its BN W
+// rows (KB8 bytes, or KB8 / 2 packed int4 bytes), with 16-byte chunk c of row r at c ^ ((r / RPL) % CPR)
+// (RPL rows per 256-byte bank line, CPR chunks per row): the fragment reads of 16 consecutive rows then hit
+// 16 distinct bank groups, and one 1 KiB copy instruction (lane i -> bytes 16 i) fills whole rows. int4
+// fragments are read as 8 bytes and widened to 16 int8 in registers (nibble n -> n | (n & 8) * 0x1e, then
+// v_perm interleaves the even-k low nibbles with the odd-k high nibbles).
+//
+// GROUP_SCALED (group == KB8 == 128): the first product of each slice starts from zero and after the slice
+// the int32 partials are folded into fp32 sums, y = fma((float)p, gs[n, slice], y), in group order; the
+// block's group scales are staged in LDS as [group][column] at the start.
 //
 // One wave per SIMD, so nothing else hides the issue time of copies and LDS reads: every copy and
 // fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
-template <int BN, int KB8, int NS, int EPI>
+template <int BN, int KB8, int NS, bool W4, int EPI>
 __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
-                                                      const float* __restrict__ ws, const half_t* __restrict__ bias, void* __restrict__ Cout, int M, int N,
-                                                      int K, const half_t* __restrict__ R, const half_t* __restrict__ G, int L) {
+                                                      const float* __restrict__ ws, const half_t* __restrict__ gs, const half_t* __restrict__ bias,
+                                                      void* __restrict__ Cout, int M, int N, int K, const half_t* __restrict__ R,
+                                                      const half_t* __restrict__ G, int L) {
     constexpr int BM = 256, TM = 128, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
-    constexpr int KS = KB8 / 32;                                   // 32-wide k steps per slice
-    constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // chunks per row, rows per copy, rows per bank line
-    constexpr int STAGE = (BM + BN) * KB8;
-    constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPI), NI = AI + BI;  // copy instructions per wave per slice
-    static_assert(BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPI) == 0, "tile");
+    constexpr bool GRP = EPI == GROUP_SCALED;
+    constexpr int KS = KB8 / 32;                                      // 32-wide k steps per slice
+    constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // A rows: chunks per row, rows per copy, rows per bank line
+    constexpr int WB = W4 ? KB8 / 2 : KB8;                            // W row bytes per slice
+    constexpr int CPRB = WB / 16, RPIB = 1024 / WB, RPLB = 256 / WB;
+    constexpr int STAGE = BM * KB8 + BN * WB;
+    constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPIB), NI = AI + BI;  // copy instructions per wave per slice
+    static_assert(BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
+    static_assert(!GRP || KB8 == 128, "one group per slice");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave >> 1, wn = wave & 1;
@@ -392,15 +406,16 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
         }
     }
     const int m0 = by * BM, n0 = bx * BN;
+    const int wrow = W4 ? K / 2 : K;  // bytes per W row in memory
 
-    // Copy instruction j of a wave fills rows (4 j + wave) RPI .. + RPI - 1 of A (or W): lane i takes row
-    // (4 j + wave) RPI + i / CPR at physical chunk i % CPR, i.e. logical chunk cchunk (the swizzle term is the
-    // same for every j). A rows past M re-read row M - 1 (their results are not stored); the clamp is folded
-    // into the per-lane offsets, taken from a clamped group base so that they are never negative (they are
-    // the unsigned 32-bit voffset of the copy).
-    const int crow = wave * RPI + lane / CPR;
-    const int cchunk = (lane % CPR) ^ ((crow / RPL) % CPR);
-    const u32 coff = (u32)crow * K + cchunk * 16;
+    // Copy instruction j of a wave fills rows (4 j + wave) RPI .. + RPI - 1 of A (or of W, with RPIB): lane i
+    // takes row (4 j + wave) RPI + i / CPR at physical chunk i % CPR, i.e. logical chunk cchunk (the swizzle
+    // term is the same for every j). A rows past M re-read row M - 1 (their results are not stored); the
+    // clamp is folded into the per-lane offsets, taken from a clamped group base so that they are never
+    // negative (they are the unsigned 32-bit voffset of the copy).
+    const int crow = wave * RPI + lane / CPR, cchunk = (lane % CPR) ^ ((crow / RPL) % CPR);
+    const int brow = wave * RPIB + lane / CPRB, bchunk = (lane % CPRB) ^ ((brow / RPLB) % CPRB);
+    const u32 boff = (u32)brow * wrow + bchunk * 16;
     int arow[AI];
     u32 aoff[AI];
 #pragma unroll
@@ -409,13 +424,13 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
         aoff[c] = (u32)(min(m0 + 4 * RPI * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
     }
     auto stage = [&](int kt) -> const char* { return smem + (kt % NS) * STAGE; };
-    // The epilogue's scales go to a scale block: ws[n0 .. n0 + BN) (BN / 64
-    // copies of 64 floats), bias[n0 ..) (256-byte copies, lanes past BN / 2 re-read the last pair) and
-    // as[m0 .. m0 + 256) (rows past M re-read row M - 1), each copy issued by one wave.
-    // (A static LDS array of its own: the compiler can then tell the epilogue's scale reads from its tile writes.)
+    // The epilogue's scales go to a scale block: ws[n0 .. n0 + BN) (BN / 64 copies of 64 floats), bias[n0 ..)
+    // (256-byte copies, lanes past BN / 2 re-read the last pair) and as[m0 .. m0 + 256) (rows past M re-read
+    // row M - 1), each copy issued by one wave. (A static LDS array of its own: the compiler can then tell the
+    // epilogue's scale reads from its tile writes.)
     __shared__ __attribute__((aligned(16))) char sc[BN * 4 + SC_BIAS(BN) + 1024];
     if (EPI != RAW_ACC) {
-        constexpr int NWS = BN / 64, NB = SC_BIAS(BN) / 256;
+        constexpr int NWS = EPI == PER_CHANNEL ? BN / 64 : 0, NB = SC_BIAS(BN) / 256;
 #pragma unroll
         for (int c = 0; c < NWS + NB + 4; c++) {
             if (c % 4 != wave) continue;
@@ -429,24 +444,53 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
             }
         }
     }
+    // GROUP_SCALED: the block's group scales, transposed to [group][column] (one group per slice), past the
+    // stages and the staged output tile.
+    constexpr int GS_OFF = ((NS * STAGE > 256 * (BN * 2 + 16) ? NS * STAGE : 256 * (BN * 2 + 16)) + 15) / 16 * 16;
+    half_t* gsl = (half_t*)(smem + GS_OFF);
+    if (GRP) {
+        const int groups = K / KB8;
+        for (int idx = t; idx < BN * groups; idx += GT) {
+            const int c = idx % BN, gi = idx / BN;
+            gsl[gi * BN + c] = gs[(size_t)(n0 + c) * groups + gi];
+        }
+    }
     auto copy = [&](int kt, int c) {  // copy instruction c (< NI) of slice kt
         const char* st = stage(kt);
-        const int k0 = kt * KB8;
-        if (c < AI) dma16(A + (size_t)arow[c] * K + k0, aoff[c], st + (4 * c + wave) * 1024);
-        else dma16(W + (size_t)(n0 + 4 * RPI * (c - AI)) * K + k0, coff, st + BM * KB8 + (4 * (c - AI) + wave) * 1024);
+        if (c < AI) dma16(A + (size_t)arow[c] * K + kt * KB8, aoff[c], st + (4 * c + wave) * 1024);
+        else dma16(W + (size_t)(n0 + 4 * RPIB * (c - AI)) * wrow + kt * WB, boff, st + BM * KB8 + (4 * (c - AI) + wave) * 1024);
     };
 
-    // Fragment f (< FI: A block f, else W block f - FI) of k step kk: row base + lq, chunk 2 kk + g.
-    const int fx = (lq / RPL) % CPR;
+    // Fragment f (< FI: A block f, else W block f - FI) of k step kk: row base + lq, k values 32 kk + 16 g ..
+    // + 15, i.e. chunk 2 kk + g of an A row, the half g of chunk kk of a packed int4 W row.
+    const int fx = (lq / RPL) % CPR, fxb = (lq / RPLB) % CPRB;
     auto frag = [&](const char* st, int kk, int f) -> i4v {
-        const u32 off = (u32)(lq * KB8 + (((2 * kk + g) ^ fx) << 4));
-        return f < FI ? *(const i4v*)(st + (wm * TM + f * 32) * KB8 + off) : *(const i4v*)(st + BM * KB8 + (wn * TN + (f - FI) * 32) * KB8 + off);
+        if (f < FI) return *(const i4v*)(st + (wm * TM + f * 32 + lq) * KB8 + (((2 * kk + g) ^ fx) << 4));
+        const char* wr = st + BM * KB8 + (wn * TN + (f - FI) * 32 + lq) * WB;
+        if (!W4) return *(const i4v*)(wr + (((2 * kk + g) ^ fxb) << 4));
+        const u2v p = *(const u2v*)(wr + ((kk ^ fxb) << 4) + 8 * g);
+        u4v o;
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+            u32 lo = p[d] & 0x0f0f0f0fu, hi = (p[d] >> 4) & 0x0f0f0f0fu;
+            lo |= (lo & 0x08080808u) * 0x1eu;
+            hi |= (hi & 0x08080808u) * 0x1eu;
+            o[2 * d] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+            o[2 * d + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+        }
+        return as_i4(o);
     };
     i16v acc[FI][FJ];
+    f16v yacc[GRP ? FI : 1][GRP ? FJ : 1];
 #pragma unroll
     for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++) acc[i][j] = (i16v){};
+    if (GRP)
+#pragma unroll
+        for (int i = 0; i < FI; i++)
+#pragma unroll
+            for (int j = 0; j < FJ; j++) yacc[GRP ? i : 0][GRP ? j : 0] = (f16v){};
     i4v fr[2][NR];  // fragments of the current and the next k step
 
     const int KT = K / KB8;
@@ -488,7 +532,8 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
             const int nc = CB(ks + 1) - CB(ks);
 #pragma unroll
             for (int p = 0; p < NF; p++) {
-                acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[cur][FI + p % FJ], fr[cur][p / FJ], acc[p / FJ][p % FJ], 0, 0, 0);
+                const i16v c0 = GRP && ks == 0 ? (i16v){} : acc[p / FJ][p % FJ];
+                acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[cur][FI + p % FJ], fr[cur][p / FJ], c0, 0, 0, 0);
                 if (AHEAD)
 #pragma unroll
                     for (int c = 0; c < nc; c++)
@@ -499,6 +544,20 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
                         if ((f * NF + NF / 2) / NR == p) fr[nxt][f] = last ? frag(sn, 0, f) : frag(st, ks + 1, f);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        }
+        if constexpr (GRP) {
+            // Fold the slice's partials: register r of block (i, j) is column wn TN + 32 j + 8 (r / 4) + 4 g + r % 4.
+#pragma unroll
+            for (int j = 0; j < FJ; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const h4v gv = *(const h4v*)(gsl + kt * BN + wn * TN + j * 32 + 8 * q + 4 * g);
+#pragma unroll
+                    for (int i = 0; i < FI; i++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e] = __builtin_fmaf((float)acc[i][j][4 * q + e], (float)gv[e], yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e]);
+                }
         }
     };
     using yes = std::integral_constant<bool, true>;
@@ -511,24 +570,27 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
         epilogue_rows<FI, FJ, EPI>(acc, lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
     } else {
         __syncthreads();  // the staged tile overlaps the stages
-        epilogue_block<BN, FI, FJ>(acc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
+        epilogue_block<BN, FI, FJ, EPI>(acc, yacc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
     }
 }
 
-template <int BN, int KB8, int NS, int EPI>
-static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
-                        const void* G, int L, void* stream) {
-    const size_t stages = (size_t)NS * (256 + BN) * KB8, tile = (size_t)256 * (BN * 2 + 16);
-    const size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
-    auto kern = gemm8_kernel<BN, KB8, NS, EPI>;
-    static bool configured = false;
-    if (!configured) {
+template <int BN, int KB8, int NS, bool W4, int EPI>
+static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
+                        const void* R, const void* G, int L, void* stream) {
+    const size_t stage = (size_t)256 * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
+    const size_t stages = NS * stage, tile = (size_t)256 * (BN * 2 + 16);
+    size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
+    if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
+    if (lds > 160 * 1024 - (size_t)(BN * 4 + SC_BIAS(BN) + 1024)) return -1;
+    auto kern = gemm8_kernel<BN, KB8, NS, W4, EPI>;
+    static int configured = 0;
+    if ((size_t)configured < lds) {
         const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return (int)e;
-        configured = true;
+        configured = (int)lds;
     }
     hipLaunchKernelGGL(kern, dim3(N / BN, (M + 255) / 256), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
-                       (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
+                       (const half_t*)gs, (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
     return (int)hipGetLastError();
 }
 
@@ -549,23 +611,31 @@ static int gemm8_width(int M, int N) {
     return best;
 }
 
-template <int EPI>
-static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* bias, void* c, int M, int N, int K, const void* R,
-                     const void* G, int L, void* stream) {
+// The direct-copy kernel for this call, or -1 when the call does not fit it (the caller then uses gemm_kernel).
+template <bool W4, int EPI>
+static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
+                     int group, const void* R, const void* G, int L, void* stream) {
     if (K >= (1 << 24)) return -1;  // per-lane copy offsets (< 64 K) must fit the 32-bit voffset
     // The row-segment epilogue reads ws as float4 and bias / R / G and writes C as 8-byte (int32: 16-byte) vectors.
-    auto aligned = [](const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; };
+    auto aligned = [](const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; };
     if (!aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
-    // 128-byte k slices in two stages when K allows, else 64-byte slices in four.
-    const bool wide = K % 128 == 0;
-    switch (gemm8_width(M, N) * 2 + (wide ? 1 : 0)) {
-        case 513: return launch_gemm8<256, 128, 2, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 385: return launch_gemm8<192, 128, 2, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 257: return launch_gemm8<128, 128, 3, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 512: return launch_gemm8<256, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 384: return launch_gemm8<192, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        case 256: return launch_gemm8<128, 64, 4, EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
-        default: return -1;
+    if constexpr (EPI == GROUP_SCALED) {
+        // One group per 128-wide slice; fp32 group sums beside the accumulators only fit 128-wide tiles.
+        if (group != 128 || K % 128 != 0 || N % 128 != 0) return -1;
+        return launch_gemm8<128, 128, 3, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+    } else {
+        // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
+        const bool wide = K % 128 == 0;
+        if (W4 && !wide) return -1;
+        switch (gemm8_width(M, N) * 2 + (wide ? 1 : 0)) {
+            case 513: return launch_gemm8<256, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 385: return launch_gemm8<192, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 257: return launch_gemm8<128, 128, 3, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 512: if constexpr (!W4) return launch_gemm8<256, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            case 384: if constexpr (!W4) return launch_gemm8<192, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            case 256: if constexpr (!W4) return launch_gemm8<128, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            default: return -1;
+        }
     }
 }
 
@@ -590,8 +660,8 @@ static int dispatch(const void* a, const void* w, const float* as, const float* 
                     int group, const void* R, const void* G, int L, void* stream) {
     if (M <= 0 || N <= 0 || K <= 0 || N % 64 != 0 || K % BK != 0) return RDA_ERR_INVALID;
     if (R && (!G || L <= 0)) return RDA_ERR_INVALID;
-    if constexpr (!W4 && EPI != GROUP_SCALED) {
-        const int e = dispatch8<EPI>(a, w, as, ws, bias, c, M, N, K, R, G, L, stream);
+    {
+        const int e = dispatch8<W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
         if (e >= 0) return e;
     }
     if constexpr (EPI == GROUP_SCALED) {
