@@ -4,7 +4,8 @@
 // are streamed once with 16-byte non-temporal loads, the activation row sits in LDS.
 #include "common.h"
 
-#define GV_WAVES 4
+#define GV_WAVES 4  // waves per block of the bf16 logits GEMV
+#define GI_WAVES 8  // waves per block of the int8 GEMV
 #define SPLITS 32  // position chunks per (batch, kv head) in attn_decode
 #define HEAD 128
 
@@ -33,50 +34,63 @@ __global__ __launch_bounds__(256) void rotate_kernel(const float* __restrict__ x
 
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 
-// out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns RW rows
-// and reads them in steps of 1024 values (16 per lane; a last half step of 512 when K % 1024 == 512).
-// All of a wave's weight loads -- at most 16 steps x rows, 16 KiB -- are issued first, before x is
-// staged, so a launch costs one memory round trip rather than one per step; the host picks RW so
-// that the loads fit (RW steps <= 16). x is fp32 or fp16; out has the dtype of x. x sits in LDS in
-// reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the f4 j of lane l
-// in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
-template <int RW, bool XH>
-__global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
+// out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns one row
+// and reads it in steps of 1024 values (16 per lane), plus a last half step of 512 (8 per lane) when
+// TAIL (K % 1024 == 512). x is fp32 or fp16; out has the dtype of x. One row per wave and 8 waves per
+// block measured fastest on the decode shapes (K = 4096, N = 1024 .. 12288): more waves in flight per CU
+// beat more rows per wave, and larger blocks (which read x fewer times) did not gain.
+//
+// One memory round trip per launch: every load of the kernel is issued at the start, x and the row scale
+// first, then the G steps of the row (the host picks G >= K / 1024). Loads complete in issue order, so
+// staging x into LDS waits for x alone and the products of a step start as soon as that step's weights
+// have arrived (sched_barrier keeps this issue order). No load sits under a branch (branches would make
+// the compiler's wait counts assume the fewest loads in flight): steps past K / 1024 re-read an in-bounds
+// chunk of the row and are skipped by the products, indices of x past K / 4 re-read x[0 .. 4).
+// x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the
+// f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
+template <int G, bool TAIL, bool XH>
+__global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
                                                                  const float* __restrict__ bias, void* __restrict__ out, int N, int K) {
-    constexpr int G = 16 / RW;  // steps whose loads are in flight together
+    constexpr int XS = (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;  // float4s of x per thread: K / 4 <= 64 GI_WAVES XS
     extern __shared__ f4 xs[];
     const int steps = K / 1024;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = (blockIdx.x * GV_WAVES + wave) * RW;
+    const int row = blockIdx.x * GI_WAVES + wave;
     const bool active = row < N;
     const int8_t* base = w + (size_t)(active ? row : 0) * K;
-    u4v v[G][RW];
-    u2v vt[RW];
+    typedef typename std::conditional<XH, h4v, f4>::type xv_t;
+    xv_t xr[XS];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-        if (g < steps)
+    for (int j = 0; j < XS; j++) {
+        const int i = threadIdx.x + j * GI_WAVES * 64;
+        xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
+    }
+    const float sc = scale[active ? row : 0];
+    __builtin_amdgcn_sched_barrier(0);  // x and the scale go out before the weights
+    u4v v[G];
+    u2v vt;
 #pragma unroll
-            for (int r = 0; r < RW; r++) v[g][r] = __builtin_nontemporal_load((const u4v*)(base + (size_t)r * K + g * 1024 + lane * 16));
-    if (K % 1024)
-#pragma unroll
-        for (int r = 0; r < RW; r++) vt[r] = __builtin_nontemporal_load((const u2v*)(base + (size_t)r * K + steps * 1024 + lane * 8));
+    for (int g = 0; g < G; g++) {
+        v[g] = __builtin_nontemporal_load((const u4v*)(base + min(g * 1024 + lane * 16, K - 16)));
+        __builtin_amdgcn_sched_barrier(0);  // step order, the order of the products
+    }
+    if constexpr (TAIL) vt = __builtin_nontemporal_load((const u2v*)(base + steps * 1024 + lane * 8));
+    __builtin_amdgcn_sched_barrier(0);
 
-    for (int i = threadIdx.x; i < K / 4; i += GV_WAVES * 64) {
-        f4 x;
-        if (XH) {
-            const h4v hv = ((const h4v*)xin)[i];
-            x = (f4){(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]};
-        } else {
-            x = ((const f4*)xin)[i];
+#pragma unroll
+    for (int j = 0; j < XS; j++) {
+        const int i = threadIdx.x + j * GI_WAVES * 64;
+        if (i < K / 4) {
+            const int tail = i - steps * 256;
+            f4 x;
+            if constexpr (XH) x = (f4){(float)xr[j][0], (float)xr[j][1], (float)xr[j][2], (float)xr[j][3]};
+            else x = xr[j];
+            xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = x;
         }
-        const int tail = i - steps * 256;
-        xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = x;
     }
     __syncthreads();
     if (!active) return;
-    float acc[RW];
-#pragma unroll
-    for (int r = 0; r < RW; r++) acc[r] = 0.f;
+    float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < G; g++) {
         if (g >= steps) continue;
@@ -84,29 +98,22 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_i8_kernel(const void* __re
         for (int j = 0; j < 4; j++) {
             const f4 xv = xs[(g * 4 + j) * 64 + lane];
 #pragma unroll
-            for (int r = 0; r < RW; r++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(v[g][r][j], i), xv[i], acc[r]);
+            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[g][j], i), xv[i], acc);
         }
     }
-    if (K % 1024) {
+    if constexpr (TAIL) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const f4 xv = xs[steps * 256 + j * 64 + lane];
 #pragma unroll
-            for (int r = 0; r < RW; r++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[r] = __builtin_fmaf(sbyte(vt[r][j], i), xv[i], acc[r]);
+            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[j], i), xv[i], acc);
         }
     }
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-        float sum = wave_sum(acc[r]) * scale[row + r];
-        if (bias) sum = sum + bias[row + r];
-        if (lane == 0) {
-            if (XH) ((half_t*)out)[row + r] = to_half(sum);
-            else ((float*)out)[row + r] = sum;
-        }
+    float sum = wave_sum(acc) * sc;
+    if (bias) sum = sum + bias[row];
+    if (lane == 0) {
+        if (XH) ((half_t*)out)[row] = to_half(sum);
+        else ((float*)out)[row] = sum;
     }
 }
 
@@ -291,12 +298,21 @@ __global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restric
     out[head * HEAD + threadIdx.x] = value / total;
 }
 
-template <int RW, bool XH>
+template <int G, bool TAIL, bool XH>
 static int launch_gemv(const void* x, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
-    const int rows = GV_WAVES * RW;
-    hipLaunchKernelGGL((gemv_i8_kernel<RW, XH>), dim3((N + rows - 1) / rows), dim3(GV_WAVES * 64), (size_t)K * 4, (hipStream_t)stream, x,
+    hipLaunchKernelGGL((gemv_i8_kernel<G, TAIL, XH>), dim3((N + GI_WAVES - 1) / GI_WAVES), dim3(GI_WAVES * 64), (size_t)K * 4, (hipStream_t)stream, x,
                        (const int8_t*)w, scale, bias, out, N, K);
     return (int)hipGetLastError();
+}
+
+template <int G>
+static int launch_gemv_g(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
+    switch ((K % 1024 ? 2 : 0) + (x_half ? 1 : 0)) {
+    case 0: return launch_gemv<G, false, false>(x, w, scale, bias, out, N, K, stream);
+    case 1: return launch_gemv<G, false, true>(x, w, scale, bias, out, N, K, stream);
+    case 2: return launch_gemv<G, true, false>(x, w, scale, bias, out, N, K, stream);
+    default: return launch_gemv<G, true, true>(x, w, scale, bias, out, N, K, stream);
+    }
 }
 
 extern "C" {
@@ -309,19 +325,12 @@ int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
 
 // x_half: 0 for fp32 x and out, 1 for fp16 x and out.
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
-    if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384 || N % 4 != 0) return RDA_ERR_INVALID;
-    // Rows per wave: as many as keep the wave's loads within 16 steps and the grid at >= 256 workgroups.
-    const int steps = (K + 1023) / 1024;
-    int rw = steps <= 4 ? 4 : steps <= 8 ? 2 : 1;
-    while (rw > 1 && (N % (GV_WAVES * rw) != 0 || N / (GV_WAVES * rw) < 256)) rw /= 2;
-    switch (rw * 2 + (x_half ? 1 : 0)) {
-    case 8: return launch_gemv<4, false>(x, w, scale, bias, out, N, K, stream);
-    case 9: return launch_gemv<4, true>(x, w, scale, bias, out, N, K, stream);
-    case 4: return launch_gemv<2, false>(x, w, scale, bias, out, N, K, stream);
-    case 5: return launch_gemv<2, true>(x, w, scale, bias, out, N, K, stream);
-    case 2: return launch_gemv<1, false>(x, w, scale, bias, out, N, K, stream);
-    default: return launch_gemv<1, true>(x, w, scale, bias, out, N, K, stream);
-    }
+    if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
+    // Steps in flight: the first of 4, 8, 16 that covers K / 1024.
+    const int steps = K / 1024;
+    if (steps <= 4) return launch_gemv_g<4>(x, x_half, w, scale, bias, out, N, K, stream);
+    if (steps <= 8) return launch_gemv_g<8>(x, x_half, w, scale, bias, out, N, K, stream);
+    return launch_gemv_g<16>(x, x_half, w, scale, bias, out, N, K, stream);
 }
 
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream) {

@@ -23,7 +23,7 @@ except ImportError:
     comfy_kitchen = comfy = None
     MixedPrecisionOp = MLP = BaseQwen3 = FixedKV = None
 
-BLOCK_ROWS = 16  # N must be a multiple: 4 waves x 4 rows per workgroup in gemv_i8 (csrc/decode.hip)
+BLOCK_ROWS = 16  # patch() eligibility: N a multiple, as in the reference (int8_gemv.py:14, 135); gemv_i8 itself takes any N
 STEP = 512  # K must be a multiple: a half step of gemv_i8 (64 lanes x 8 int8)
 BF16_STEP = 256  # K granularity of gemv_bf16 (64 lanes x 4 bf16)
 SPLITS = 32  # position chunks per KV head in attn_decode (SPLITS in csrc/decode.hip)

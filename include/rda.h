@@ -103,7 +103,7 @@ int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, 
 int rda_rotate(const float* x, float* out, int rows, int group, void* stream);
 
 /* gemv_i8, int8_gemv.py:60-63 (int8_gemv.hip:54-85): out[n] = scale[n] * dot(w[n], x) (+ bias[n]).
- * x_half = 0: x, out fp32; x_half = 1: x, out fp16. K % 512 == 0, K <= 16384, N % 4 == 0. */
+ * x_half = 0: x, out fp32; x_half = 1: x, out fp16. K % 512 == 0, K <= 16384. */
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream);
 
 /* gemv_bf16, int8_gemv.py:97 (int8_gemv.hip:87-119): fp32 logits of a bf16 table. K % 256 == 0, N % 8 == 0. */
