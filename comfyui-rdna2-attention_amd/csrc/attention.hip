@@ -5,18 +5,19 @@
 // Arithmetic follows attn / attn_i8 (hip_attention.hip:160-373): scores s in fp32; the running
 // maximum m only moves when some row's block maximum exceeds m + 8 (the lazy rescale,
 // hip_attention.hip:333-340); p = exp2(s * scale_log2 - m) (int8: exp2(s - m) with s already
-// scaled); l sums the fp32 p; P is rounded to fp16 before PV; out = fp16(o * (1 / l)).
+// scaled); P is rounded to fp16 before PV and l sums those fp16 values (in fp32, by v_dot2 with
+// ones, which halves the adds; the reference sums the fp32 p); out = fp16(o * (1 / l)).
 //
-// Work split. A workgroup of eight wave64s owns 128 query rows of one (batch, head). The waves
-// form two groups of four that walk the two halves of the key range; inside a group each wave
-// owns 32 query rows and keeps Q, O, l and m for them in registers (about 200 VGPRs, so two
-// waves share each SIMD: one's softmax runs while the other's products keep the matrix core
-// busy). At the end the second group's (m, l, O) is merged into the first through LDS. With
-// 128-row blocks the attention configuration (24 heads x 4096 rows) is 768 workgroups, three per
-// CU, one resident at a time. Block ids are remapped so that the workgroups an XCD runs together
-// belong to one head and share its K/V through that XCD's L2.
+// Work split. A workgroup of four wave64s owns 128 query rows of one (batch, head) and walks the
+// whole key range; each wave owns 32 query rows and keeps Q, O, l and m for them in registers
+// (<= 168 VGPRs). Three workgroups share a CU (three waves per SIMD, 2 x 16 KiB of LDS each), so
+// the attention configuration (24 heads x 4096 rows = 768 workgroups) runs in one round, and
+// while one workgroup waits at its barrier or for LDS, the others keep the matrix cores busy
+// (one eight-wave workgroup per CU, with two waves per SIMD in lockstep between barriers, left
+// the matrix cores idle for half the cycles). Block ids are remapped so that the workgroups an
+// XCD runs together belong to one head and share its K/V through that XCD's L2.
 //
-// Tiles. Each group double-buffers 64-key tiles of K and V in LDS. They are copied by direct
+// Tiles. Each workgroup double-buffers 32-key tiles of K and V in LDS. They are copied by direct
 // global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes at LDS
 // base + 16 i), issued one whole tile ahead, so no register holds a tile in flight and the
 // load latency hides behind a full tile of work; the s_waitcnt before each tile's closing
@@ -36,10 +37,9 @@
 // i % 4 of the 8-byte read of lane 4 e + i / 4 as its element e.
 #include "common.h"
 
-#define AT 512  // threads per workgroup: two groups of four waves
-#define GT 256  // threads per group
+#define AT 256  // threads per workgroup: four waves
 #define QB 128  // query rows per workgroup (32 per wave)
-#define KB 64   // keys per tile
+#define KB 32   // keys per tile
 
 struct AttnArgs {
     const half_t* q;
@@ -56,12 +56,11 @@ struct AttnArgs {
 template <bool I8>
 struct Tile {
     static constexpr int K_ROW = I8 ? 128 : 256;
-    static constexpr int K_BYTES = KB * K_ROW + (I8 ? KB * 4 : 0);  // K rows, then the int8 per-key scales
-    static constexpr int BYTES = K_BYTES + KB * 256;                // one stage: K, then V
-    static constexpr int STAGES = 4 * BYTES;                        // two stages per group
-    static constexpr int MERGE_LANE = 68;                           // floats per lane: O (64), m, l, pad
-    static constexpr int MERGE = 4 * 64 * MERGE_LANE * 4;           // (O, m, l) of the second group's waves
-    static constexpr int LDS = STAGES > MERGE ? STAGES : MERGE;
+    static constexpr int SC_BYTES = I8 ? 256 : 0;  // int8 per-key scales: one 256-byte copy, KB floats used
+    static constexpr int K_BYTES = KB * K_ROW + SC_BYTES;
+    static constexpr int V_BYTES = KB * 256;
+    static constexpr int BYTES = K_BYTES + V_BYTES;  // one stage: K, then V
+    static constexpr int LDS = 2 * BYTES;
 };
 
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -78,11 +77,11 @@ __device__ __forceinline__ f2 halves(float x) {
 }
 
 template <bool I8>
-__global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_kernel(AttnArgs p) {
+__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_kernel(AttnArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     using T = Tile<I8>;
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, lq = lane & 31;
-    const int wave_u = __builtin_amdgcn_readfirstlane(t >> 6), wq = wave_u & 3, grp = wave_u >> 2;  // scalars
+    const int wq = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar
 
     // Block remap: consecutive block ids go round-robin to the 8 XCDs; give each XCD a contiguous run
     // of (head, q-block) work so its resident workgroups share K/V through its L2.
@@ -150,15 +149,13 @@ __global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const int bkv = b * p.Hkv + hk;
     const int8_t* k8base = I8 ? p.k8 + (size_t)bkv * p.Lk_pad * 128 : nullptr;
     const float* ksbase = I8 ? p.ks + (size_t)bkv * p.Lk_pad : nullptr;
+    const int tiles = (p.Lk + KB - 1) / KB;
 
-    const int tiles = (p.Lk + KB - 1) / KB, half = (tiles + 1) / 2;
-    const int t_begin = grp * half, t_end = min(tiles, t_begin + half);
-
-    // Copies the tile at key0 into stage st; the group's four waves take every fourth 1 KiB block, so
-    // DMA i of a wave fills K (and V) rows 16 i + row0 .. +3, row0 = 4 wq + lane / 16. Rows past Lk
-    // re-read row Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite) values
-    // drop out. int8 K is zero-padded to a whole tile by pack_k_i8. Per-lane byte offsets are fixed;
-    // only the tile base moves (the launcher keeps 64 rows of stride inside 2^31 bytes).
+    // Copies the tile at key0 into stage st; DMA i (< 2) of a wave fills K (and V) rows 16 i + row0 .. +3,
+    // row0 = 4 wq + lane / 16 (int8 K: one DMA per wave, rows 8 wq + lane / 8). Rows past Lk re-read row
+    // Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite) values drop out. int8 K is
+    // zero-padded to a whole tile by pack_k_i8. Per-lane byte offsets are fixed; only the tile base moves
+    // (the launcher keeps 32 rows of stride inside 2^31 bytes).
     const int row0 = 4 * wq + (lane >> 4);
     const long skl2 = p.skl * 2, svl2 = p.svl * 2;
     const int kc = (lane & 15) ^ row0, vc = (lane & 15) ^ ((lane >> 4) << 2);
@@ -167,23 +164,21 @@ __global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const u32 k8_off = (u32)((8 * wq + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
     auto issue = [&](int key0, const char* st) {
         if (I8) {
-            const char* kt = (const char*)k8base + (size_t)key0 * 128;
-#pragma unroll
-            for (int i = 0; i < 2; i++) dma16(kt + i * 4096, k8_off, st + (4 * i + wq) * 1024);
-            if (wq == 0) dma4(ksbase + key0, lane * 4, st + KB * 128);
+            dma16((const char*)k8base + (size_t)key0 * 128, k8_off, st + wq * 1024);
+            if (wq == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, st + KB * 128);
         }
         if (key0 + KB <= p.Lk) {
             const char* kt = (const char*)kbase + key0 * skl2;
             const char* vt = (const char*)vbase + key0 * svl2;
             if (!I8) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + wq) * 1024);
+                for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + wq) * 1024);
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
+            for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < 2; i++) {
                 const int key = min(key0 + 16 * i + row0, p.Lk - 1);
                 if (!I8) dma16_at(kbase + (long)key * p.skl + kc * 8, st + (4 * i + wq) * 1024);
                 dma16_at(vbase + (long)key * p.svl + vc * 8, st + T::K_BYTES + (4 * i + wq) * 1024);
@@ -192,76 +187,59 @@ __global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     };
 
     // S^T of the tile in stage st (scaled for int8), into s.
-    float s[2][16];  // [kb][r]
+    float s[16];
     auto scores = [&](const char* st) {
         if (!I8) {
-            // K operands in two batches of eight reads; each batch goes out before the products that use it.
+            // K operands in two batches of four reads; each batch goes out before the products that use it.
             // Lane-dependent parts of the addresses are recomputed here from an opaque copy of the lane id:
-            // hoisted out of the tile loop they would hold a dozen VGPRs for its whole length.
+            // hoisted out of the tile loop they would hold VGPRs for its whole length.
             int ln = lane;
             asm volatile("" : "+v"(ln));
             const char* krow = st + (ln & 31) * 256;
             const int kx = (ln & 15) ^ (ln >> 5);  // chunk 2 ks + g sits at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx
-            f16v acc[2] = {};
+            f16v acc = {};
 #pragma unroll
             for (int half_k = 0; half_k < 2; half_k++) {
-                h8 ka[4][2];
+                h8 ka[4];
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++)
-#pragma unroll
-                    for (int kb = 0; kb < 2; kb++) {
-                        const int ks = half_k * 4 + k4;
-                        ka[k4][kb] = *(const h8*)(krow + kb * 32 * 256 + (((2 * ks) ^ kx) << 4));
-                    }
+                for (int k4 = 0; k4 < 4; k4++) ka[k4] = *(const h8*)(krow + (((2 * (half_k * 4 + k4)) ^ kx) << 4));
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++)
-#pragma unroll
-                    for (int kb = 0; kb < 2; kb++) acc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4][kb], qf[half_k * 4 + k4], acc[kb], 0, 0, 0);
+                for (int k4 = 0; k4 < 4; k4++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4], qf[half_k * 4 + k4], acc, 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[kb][r] = acc[kb][r];
+            for (int r = 0; r < 16; r++) s[r] = acc[r];
         } else {
             const float* kscale = (const float*)(st + KB * 128);
-            i4v ka[4][2];
+            i4v ka[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-                for (int kb = 0; kb < 2; kb++) ka[ks][kb] = *(const i4v*)(st + (kb * 32 + lq) * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(st + lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
             __builtin_amdgcn_sched_barrier(0);
-            i16v acc[2] = {};
+            i16v acc = {};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
+            for (int ks = 0; ks < 4; ks++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
 #pragma unroll
-                for (int kb = 0; kb < 2; kb++) acc[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks][kb], q8f[ks], acc[kb], 0, 0, 0);
+            for (int r4 = 0; r4 < 4; r4++) {
+                const f4 sc = *(const f4*)(kscale + 8 * r4 + 4 * g);
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    const f4 sc = *(const f4*)(kscale + kb * 32 + 8 * r4 + 4 * g);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) s[kb][r4 * 4 + e] = (float)acc[kb][r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
-                }
+                for (int e = 0; e < 4; e++) s[r4 * 4 + e] = (float)acc[r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
+            }
         }
     };
-    // Masking, the online softmax and O^T += V^T P^T for the tile at key0 in stage st, from s.
-    auto update = [&](const char* st, int key0) {
+    // Masking (mask: the tile may reach past Lk) and the online softmax for the tile at key0, from s: updates
+    // m, l and O's scale and leaves P in pf.
+    h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
+    auto softmax = [&](int key0, auto mask) {
         // Keys past Lk (hip_attention.hip:324-328).
-        if (key0 + KB > p.Lk) {
+        if (decltype(mask)::value && key0 + KB > p.Lk) {
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                    if (key0 + kb * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[kb][r] = -1e30f;
+            for (int r = 0; r < 16; r++)
+                if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[r] = -1e30f;
         }
-        float mx = s[0][0];
+        float mx = s[0];
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb][r]);
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[r]);
         const f2 mh = halves(mx);
         mx = fmaxf(mh[0], mh[1]);
         if (!I8) mx *= p.scale_log2;
@@ -272,12 +250,23 @@ __global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
             for (int i = 0; i < 4; i++) o[i] *= alpha;
         }
-        // V^T operands in four batches of four products; the first batch goes out before the P arithmetic,
-        // which hides its latency, each later one before the products of the batch ahead of it.
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            const float e0 = I8 ? __builtin_amdgcn_exp2f(s[r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.scale_log2, -m));
+            const float e1 = I8 ? __builtin_amdgcn_exp2f(s[r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], p.scale_log2, -m));
+            const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
+            l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);  // l sums the fp16 P of PV
+            pf[r >> 3][r & 7] = pk[0];
+            pf[r >> 3][(r & 7) + 1] = pk[1];
+        }
+    };
+    // O^T += V^T P^T with the V tile in vst and P in pf; the second step's V^T operands are read while the
+    // first step's products run.
+    auto pv = [&](const char* vst) {
         int ln = lane;  // opaque lane id, as in scores
         asm volatile("" : "+v"(ln));
         const int sg = ln & 15;
-        const char* vt = st + T::K_BYTES + (4 * (ln >> 5) + (sg >> 2)) * 256 + (sg & 1) * 8;
+        const char* vt = vst + (4 * (ln >> 5) + (sg >> 2)) * 256 + (sg & 1) * 8;
         const int vx = (2 * ((ln >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
         auto read_v = [&](h8 (&va)[4], int j) {
 #pragma unroll
@@ -288,77 +277,46 @@ __global__ __launch_bounds__(AT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         };
         h8 va[2][4];
         read_v(va[0], 0);
+        read_v(va[1], 1);
         __builtin_amdgcn_sched_barrier(0);
-        // P, packed for the four 16-key steps: step j holds registers 8 (j % 2) .. +8 of block j / 2.
-        h8 pf[4];
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-                const float e0 = I8 ? __builtin_amdgcn_exp2f(s[kb][r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], p.scale_log2, -m));
-                const float e1 = I8 ? __builtin_amdgcn_exp2f(s[kb][r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], p.scale_log2, -m));
-                l += e0 + e1;
-                const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
-                pf[kb * 2 + (r >> 3)][r & 7] = pk[0];
-                pf[kb * 2 + (r >> 3)][(r & 7) + 1] = pk[1];
-            }
-        // O^T += V^T P^T.
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (j < 3) read_v(va[(j + 1) & 1], j + 1);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[j & 1][dt], pf[j], o[dt], 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+            for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[j][dt], pf[j], o[dt], 0, 0, 0);
     };
 
     // Tile loop: the copies of tile i + 1 go out before the work on tile i and are awaited at its closing
-    // barrier, which also retires every read of the stage the next copies overwrite. Both groups run
-    // `half` iterations (the second may have one tile fewer) so that every wave reaches every barrier.
-    const int n = t_end - t_begin;  // tiles of this group: half for group 0, half or half - 1 for group 1
-    const char* gbuf = smem + grp * 2 * T::BYTES;
-    auto stage = [&](int i) -> const char* { return gbuf + (i & 1) * T::BYTES; };
-    if (n > 0) issue(t_begin * KB, stage(0));
+    // barrier, which also retires every read of the stage the next copies overwrite. The last tile -- the
+    // only one that can reach past Lk -- is peeled off with the masking (under a runtime test the compiler
+    // turns the masking into selects on every tile).
+    auto stage = [&](int i) -> const char* { return smem + (i & 1) * T::BYTES; };
+    issue(0, stage(0));
     wait_copies();
     __syncthreads();
-    for (int i = 0; i < half; i++) {
-        if (i < n) {
-            if (i + 1 < n) issue((t_begin + i + 1) * KB, stage(i + 1));
-            scores(stage(i));
-            update(stage(i), (t_begin + i) * KB);
-        }
+    for (int i = 0; i < tiles - 1; i++) {
+        issue((i + 1) * KB, stage(i + 1));
+        scores(stage(i));
+        softmax(i * KB, std::false_type{});
+        pv(stage(i) + T::K_BYTES);
         wait_copies();
         __syncthreads();
     }
-    __syncthreads();  // every stage read retires before the merge area (which overlaps the stages) is written
+    scores(stage(tiles - 1));
+    softmax((tiles - 1) * KB, std::true_type{});
+    pv(stage(tiles - 1) + T::K_BYTES);
 
-    // Merge the second group's (m, l, O) into the first group's, then normalise and store.
-    float* mb = (float*)smem + (wq * 64 + lane) * T::MERGE_LANE;
-    if (grp == 1) {
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int r = 0; r < 16; r += 4) *(f4*)(mb + dt * 16 + r) = (f4){o[dt][r], o[dt][r + 1], o[dt][r + 2], o[dt][r + 3]};
-        mb[64] = m;
-        mb[65] = l;
-    }
-    __syncthreads();
-    if (grp == 1) return;
-    const float m1 = mb[64], l1 = mb[65];
-    const float mn = fmaxf(m, m1), a0 = __builtin_amdgcn_exp2f(m - mn), a1 = __builtin_amdgcn_exp2f(m1 - mn);
-    const f2 lh = halves(l * a0 + l1 * a1);
-    const float inv = 1.f / (lh[0] + lh[1]);  // the lane halves hold disjoint keys of one row
+    // Normalise and store: the lane halves hold disjoint keys of one row.
+    const f2 lh = halves(l);
+    const float inv = 1.f / (lh[0] + lh[1]);
     const int row = q0 + lq;
     half_t* op = p.o + b * p.sob + h * p.soh + (long)row * p.sol;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
         for (int r4 = 0; r4 < 4; r4++) {
-            const f4 o1 = *(const f4*)(mb + dt * 16 + r4 * 4);
             h4v w;
 #pragma unroll
-            for (int e = 0; e < 4; e++) w[e] = to_half((o[dt][r4 * 4 + e] * a0 + o1[e] * a1) * inv);
+            for (int e = 0; e < 4; e++) w[e] = to_half(o[dt][r4 * 4 + e] * inv);
             if (row < p.Lq) *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
         }
 }
@@ -434,7 +392,7 @@ static int launch_attn(const AttnArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-// Row strides of K and V must keep a tile's 64 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
+// Row strides of K and V must keep a tile's 32 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
 static bool attn_shapes_ok(int B, int H, int Hkv, int Lq, int Lk, const long* st) {
     const bool rows_ok = st[5] >= 0 && st[5] < (1L << 24) && st[8] >= 0 && st[8] < (1L << 24);
     return B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && Lq > 0 && Lk > 0 && (long)B * H * ((Lq + QB - 1) / QB) < (1L << 31) && rows_ok;
