@@ -120,6 +120,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             qmax = fmaxf(qh[0], qh[1]);
             const float q_scale = fmaxf(qmax / 127.f, 1e-30f);  // hip_attention.hip:183
             score_scale = q_scale * p.scale_log2;
+            const float q_rcp = 1.f / q_scale;
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 u4v w;
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
                     for (int e = 0; e < 4; e++) {
                         const int idx = d * 4 + e;
                         const float f = (float)raw[2 * ks + (idx >> 3)][idx & 7];
-                        x |= (u32)((int)rintf(f / q_scale) & 255) << (e * 8);  // hip_attention.hip:192
+                        x |= (u32)((int)rintf(div_by_scale(f, q_scale, q_rcp)) & 255) << (e * 8);  // f / q_scale, hip_attention.hip:192
                     }
                     w[d] = x;
                 }
@@ -343,13 +344,13 @@ __global__ __launch_bounds__(256) void pack_k_i8_kernel(const half_t* __restrict
     }
 #pragma unroll
     for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
-    const float scale = fmaxf(mx / 127.f, 1e-30f);
+    const float scale = fmaxf(mx / 127.f, 1e-30f), rcp = 1.f / scale;
     u2v w;
 #pragma unroll
     for (int d = 0; d < 2; d++) {
         u32 x = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) x |= (u32)((int)rintf(f[d * 4 + i] / scale) & 255) << (i * 8);
+        for (int i = 0; i < 4; i++) x |= (u32)((int)rintf(div_by_scale(f[d * 4 + i], scale, rcp)) & 255) << (i * 8);  // f / scale
         w[d] = x;
     }
     *(u2v*)(K8 + ((size_t)bkv * Lk_pad + key) * 128 + sub * 8) = w;

@@ -215,6 +215,7 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
     const float scale = I4 ? fmaxf(mx, 1e-10f) / 7.f : fmaxf(mx / 127.f, 1e-30f);
     if (t == 0) as[row] = scale;
 
+    const float rcp = 1.f / scale;
     int8_t* out = Aq + (size_t)row * K;
     for (int ch = t; ch < K / 16; ch += QT) {
         const h8 lo = ((const h8*)rotated)[ch * 2], hi = ((const h8*)rotated)[ch * 2 + 1];
@@ -222,8 +223,9 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float f = (float)(i < 8 ? lo[i] : hi[i - 8]);
-            if (I4) q[i] = (int)fminf(fmaxf(rintf(f / scale), -7.f), 7.f);  // int8_gemm.hip:84
-            else q[i] = (int)fminf(fmaxf(floorf(f / scale + 0.5f), -128.f), 127.f);  // int8_gemm.hip:53
+            const float d = div_by_scale(f, scale, rcp);  // f / scale
+            if (I4) q[i] = (int)fminf(fmaxf(rintf(d), -7.f), 7.f);  // int8_gemm.hip:84
+            else q[i] = (int)fminf(fmaxf(floorf(d + 0.5f), -128.f), 127.f);  // int8_gemm.hip:53
         }
         u4v o;
 #pragma unroll
