@@ -293,14 +293,14 @@ __device__ __forceinline__ void epilogue_rows(const i16v (&acc)[FI][FJ], int lan
     }
 }
 
-// Epilogue of the whole 256 x BN block through LDS: every wave dequantizes its C^T accumulators
+// Epilogue of the whole BM x BN block through LDS: every wave dequantizes its C^T accumulators
 // (epilogue_rows' register layout; scales and biases from the scale block `sc` in LDS; GROUP_SCALED: the
 // fp32 group sums yacc, times as) into an fp16 tile in LDS, then all 256 threads store it in 16-byte
 // chunks, consecutive lanes covering consecutive bytes of a row, so each store instruction writes whole
 // 128-byte lines (the register layout would touch 32 rows per instruction). R and G are read the same way.
 // Bytes of the bias area of the scale block: BN halfs, copied in 256-byte instructions.
 constexpr int SC_BIAS(int bn) { return (bn * 2 + 255) / 256 * 256; }
-template <int BN, int FI, int FJ, int EPI>
+template <int BM, int BN, int FI, int FJ, int EPI>
 __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const f16v (&yacc)[EPI == GROUP_SCALED ? FI : 1][EPI == GROUP_SCALED ? FJ : 1],
                                                char* tile, const char* sc, int t, int lane, int wm, int wn, int m0, int n0, int M, int N,
                                                const float* __restrict__ as, const float* __restrict__ ws, const half_t* __restrict__ bias,
@@ -341,7 +341,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
     else dequantize(std::integral_constant<bool, false>{});
     __syncthreads();
 #pragma unroll 4
-    for (int idx = t; idx < 256 * CPR; idx += GT) {
+    for (int idx = t; idx < BM * CPR; idx += GT) {
         const int r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
         if (m >= M) continue;
         h8 y = *(const h8*)(tile + r * TP + c * 2);
@@ -356,15 +356,18 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 }
 
 // int8 GEMM with direct global->LDS copies, for int8 or packed int4 weights (PER_CHANNEL, GROUP_SCALED and
-// RAW_ACC epilogues). A workgroup of four wave64s computes a 256 x BN tile, each wave a 128 x BN/2 quarter
+// RAW_ACC epilogues). A workgroup of four wave64s computes a BM x BN tile, each wave a BM/2 x BN/2 quarter
 // of 32x32 blocks (accumulators in AGPRs; the products compute W A^T, so each lane ends up owning row
 // segments of C). K advances in slices of KB8 values through NS LDS stages: the copies of slice k + NS - 1
-// go out while slice k is multiplied. A stage holds the slice's 256 A rows (KB8 bytes each), then its BN W
+// go out while slice k is multiplied. A stage holds the slice's BM A rows (KB8 bytes each), then its BN W
 // rows (KB8 bytes, or KB8 / 2 packed int4 bytes), with 16-byte chunk c of row r at c ^ ((r / RPL) % CPR)
 // (RPL rows per 256-byte bank line, CPR chunks per row): the fragment reads of 16 consecutive rows then hit
 // 16 distinct bank groups, and one 1 KiB copy instruction (lane i -> bytes 16 i) fills whole rows. int4
-// fragments are read as 8 bytes and widened to 16 int8 in registers (nibble n -> n | (n & 8) * 0x1e, then
-// v_perm interleaves the even-k low nibbles with the odd-k high nibbles).
+// fragments are read as 8 bytes and widened to 16 int8 in registers with each nibble in the high half of its
+// byte, i.e. as 16 times its signed value (two ANDs and a shift, then v_perm interleaves the even-k low
+// nibbles with the odd-k high nibbles); the accumulators then hold exactly 16 times the products, which the
+// kernel undoes after the K loop (an arithmetic shift of the int32 sums, a factor 1/16 on the fp32 group
+// sums: both exact). The host keeps K <= 65536 on this path so that 16 times the sums fits in 32 bits.
 //
 // GROUP_SCALED (group == KB8 == 128): the first product of each slice starts from zero and after the slice
 // the int32 partials are folded into fp32 sums, y = fma((float)p, gs[n, slice], y), in group order; the
@@ -374,12 +377,12 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 // fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
-template <int BN, int KB8, int NS, bool W4, int EPI>
-__global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB>
+__global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
                                                       const float* __restrict__ ws, const half_t* __restrict__ gs, const half_t* __restrict__ bias,
                                                       void* __restrict__ Cout, int M, int N, int K, const half_t* __restrict__ R,
                                                       const half_t* __restrict__ G, int L) {
-    constexpr int BM = 256, TM = 128, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
+    constexpr int TM = BM / 2, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
     constexpr bool GRP = EPI == GROUP_SCALED;
     constexpr int KS = KB8 / 32;                                      // 32-wide k steps per slice
     constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // A rows: chunks per row, rows per copy, rows per bank line
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
     constexpr int CPRB = WB / 16, RPIB = 1024 / WB, RPLB = 256 / WB;
     constexpr int STAGE = BM * KB8 + BN * WB;
     constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPIB), NI = AI + BI;  // copy instructions per wave per slice
-    static_assert(BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
+    static_assert((BM == 256 || BM == 128) && BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
     static_assert(!GRP || KB8 == 128, "one group per slice");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
@@ -425,14 +428,14 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
     }
     auto stage = [&](int kt) -> const char* { return smem + (kt % NS) * STAGE; };
     // The epilogue's scales go to a scale block: ws[n0 .. n0 + BN) (BN / 64 copies of 64 floats), bias[n0 ..)
-    // (256-byte copies, lanes past BN / 2 re-read the last pair) and as[m0 .. m0 + 256) (rows past M re-read
+    // (256-byte copies, lanes past BN / 2 re-read the last pair) and as[m0 .. m0 + BM) (rows past M re-read
     // row M - 1), each copy issued by one wave. (A static LDS array of its own: the compiler can then tell the
     // epilogue's scale reads from its tile writes.)
-    __shared__ __attribute__((aligned(16))) char sc[BN * 4 + SC_BIAS(BN) + 1024];
+    __shared__ __attribute__((aligned(16))) char sc[BN * 4 + SC_BIAS(BN) + BM * 4];
     if (EPI != RAW_ACC) {
         constexpr int NWS = EPI == PER_CHANNEL ? BN / 64 : 0, NB = SC_BIAS(BN) / 256;
 #pragma unroll
-        for (int c = 0; c < NWS + NB + 4; c++) {
+        for (int c = 0; c < NWS + NB + BM / 64; c++) {
             if (c % 4 != wave) continue;
             if (c < NWS) {
                 dma4(ws + n0 + 64 * c, lane * 4, sc + c * 256);
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
     }
     // GROUP_SCALED: the block's group scales, transposed to [group][column] (one group per slice), past the
     // stages and the staged output tile.
-    constexpr int GS_OFF = ((NS * STAGE > 256 * (BN * 2 + 16) ? NS * STAGE : 256 * (BN * 2 + 16)) + 15) / 16 * 16;
+    constexpr int GS_OFF = ((NS * STAGE > BM * (BN * 2 + 16) ? NS * STAGE : BM * (BN * 2 + 16)) + 15) / 16 * 16;
     half_t* gsl = (half_t*)(smem + GS_OFF);
     if (GRP) {
         const int groups = K / KB8;
@@ -472,9 +475,7 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
         u4v o;
 #pragma unroll
         for (int d = 0; d < 2; d++) {
-            u32 lo = p[d] & 0x0f0f0f0fu, hi = (p[d] >> 4) & 0x0f0f0f0fu;
-            lo |= (lo & 0x08080808u) * 0x1eu;
-            hi |= (hi & 0x08080808u) * 0x1eu;
+            const u32 lo = (p[d] << 4) & 0xf0f0f0f0u, hi = p[d] & 0xf0f0f0f0u;  // 16 x (signed nibble) per byte
             o[2 * d] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
             o[2 * d + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
         }
@@ -566,30 +567,43 @@ __global__ __launch_bounds__(GT, 1) void gemm8_kernel(const int8_t* __restrict__
     for (; kt + NS - 1 < KT; kt++) slice(kt, yes{}, yes{});
     for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{});
     slice(kt, no{}, no{});
+    if constexpr (W4) {  // the int4 operands were 16 times their values: undo it (exactly)
+        if constexpr (GRP) {
+#pragma unroll
+            for (int i = 0; i < FI; i++)
+#pragma unroll
+                for (int j = 0; j < FJ; j++) yacc[GRP ? i : 0][GRP ? j : 0] *= 0.0625f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < FI; i++)
+#pragma unroll
+                for (int j = 0; j < FJ; j++) acc[i][j] >>= 4;
+        }
+    }
     if constexpr (EPI == RAW_ACC) {
         epilogue_rows<FI, FJ, EPI>(acc, lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
     } else {
         __syncthreads();  // the staged tile overlaps the stages
-        epilogue_block<BN, FI, FJ, EPI>(acc, yacc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
+        epilogue_block<BM, BN, FI, FJ, EPI>(acc, yacc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
     }
 }
 
-template <int BN, int KB8, int NS, bool W4, int EPI>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                         const void* R, const void* G, int L, void* stream) {
-    const size_t stage = (size_t)256 * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
-    const size_t stages = NS * stage, tile = (size_t)256 * (BN * 2 + 16);
+    const size_t stage = (size_t)BM * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
+    const size_t stages = NS * stage, tile = (size_t)BM * (BN * 2 + 16);
     size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
     if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
-    if (lds > 160 * 1024 - (size_t)(BN * 4 + SC_BIAS(BN) + 1024)) return -1;
-    auto kern = gemm8_kernel<BN, KB8, NS, W4, EPI>;
+    if (lds > 160 * 1024 / MINB - (size_t)(BN * 4 + SC_BIAS(BN) + BM * 4)) return -1;
+    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB>;
     static int configured = 0;
     if ((size_t)configured < lds) {
         const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return (int)e;
         configured = (int)lds;
     }
-    hipLaunchKernelGGL(kern, dim3(N / BN, (M + 255) / 256), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
+    hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
                        (const half_t*)gs, (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
     return (int)hipGetLastError();
 }
@@ -616,24 +630,26 @@ template <bool W4, int EPI>
 static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                      int group, const void* R, const void* G, int L, void* stream) {
     if (K >= (1 << 24)) return -1;  // per-lane copy offsets (< 64 K) must fit the 32-bit voffset
+    if (W4 && K > 65536) return -1;  // 16 x the int4 products, summed over K, must fit in int32
     // The row-segment epilogue reads ws as float4 and bias / R / G and writes C as 8-byte (int32: 16-byte) vectors.
     auto aligned = [](const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; };
     if (!aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
     if constexpr (EPI == GROUP_SCALED) {
-        // One group per 128-wide slice; fp32 group sums beside the accumulators only fit 128-wide tiles.
+        // One group per 128-wide slice. 128 x 128 blocks (64 x 64 per wave) leave room for two blocks per CU, so
+        // one block's group folds (vector ALU) overlap the other's products.
         if (group != 128 || K % 128 != 0 || N % 128 != 0) return -1;
-        return launch_gemm8<128, 128, 3, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        return launch_gemm8<128, 128, 128, 3, W4, EPI, 2>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
     } else {
         // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
         const bool wide = K % 128 == 0;
         if (W4 && !wide) return -1;
         switch (gemm8_width(M, N) * 2 + (wide ? 1 : 0)) {
-            case 513: return launch_gemm8<256, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
-            case 385: return launch_gemm8<192, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
-            case 257: return launch_gemm8<128, 128, 3, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
-            case 512: if constexpr (!W4) return launch_gemm8<256, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
-            case 384: if constexpr (!W4) return launch_gemm8<192, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
-            case 256: if constexpr (!W4) return launch_gemm8<128, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            case 513: return launch_gemm8<256, 256, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 385: return launch_gemm8<256, 192, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 257: return launch_gemm8<256, 128, 128, 3, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            case 512: if constexpr (!W4) return launch_gemm8<256, 256, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            case 384: if constexpr (!W4) return launch_gemm8<256, 192, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
+            case 256: if constexpr (!W4) return launch_gemm8<256, 128, 64, 4, false, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream); return -1;
             default: return -1;
         }
     }
