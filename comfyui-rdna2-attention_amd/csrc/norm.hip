@@ -21,13 +21,27 @@ __global__ __launch_bounds__(NT) void norm_kernel(const half_t* __restrict__ X, 
     // Heads go first, so a block reads neighbouring heads of one token.
     const int h = n % H, l = (n / H) % L, b = n / H / L;
     const h8* x = (const h8*)(X + b * sb + h * sh + l * sl);
+    // Every load is issued up front, x then the weight, with no load under a branch (chunks past D / 8
+    // re-read chunk 0 and are not used), so the weight arrives during the reduction instead of after it;
+    // the host picks CHUNKS as the chunks D needs per thread.
     h8 v[CHUNKS];
+    f4 wv[CHUNKS][2];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int i = t + c * TPR;
+        v[c] = x[i < D / 8 ? i : 0];
+    }
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int i = t + c * TPR, iw = i < D / 8 ? i : 0;
+        wv[c][0] = ((const f4*)W)[iw * 2];
+        wv[c][1] = ((const f4*)W)[iw * 2 + 1];
+    }
     float sum = 0.f;
 #pragma unroll
     for (int c = 0; c < CHUNKS; c++) {
         const int i = t + c * TPR;
         if (i < D / 8) {
-            v[c] = x[i];
 #pragma unroll
             for (int j = 0; j < 8; j++) sum = __builtin_fmaf((float)v[c][j], (float)v[c][j], sum);
         }
@@ -47,7 +61,7 @@ __global__ __launch_bounds__(NT) void norm_kernel(const half_t* __restrict__ X, 
     for (int c = 0; c < CHUNKS; c++) {
         const int i = t + c * TPR;
         if (i < D / 8) {
-            const f4 lo = ((const f4*)W)[i * 2], hi = ((const f4*)W)[i * 2 + 1];
+            const f4 lo = wv[c][0], hi = wv[c][1];
             h8 o;
 #pragma unroll
             for (int j = 0; j < 8; j++) o[j] = to_half((float)v[c][j] * rstd * ((j < 4 ? lo[j & 3] : hi[j & 3]) + 1.f));
@@ -86,9 +100,18 @@ int rda_rms_norm_head(const void* x, const float* w, void* y, int B, int H, int 
 int rda_rms_norm_row(const void* x, const float* w, void* y, int B, int H, int L, int D, long sb, long sh, long sl, float eps, void* stream) {
     if (!norm_ok(B, H, L, D) || D > 8192) return RDA_ERR_INVALID;
     const int rows = B * H * L;
-    hipLaunchKernelGGL((norm_kernel<NT, 4, false>), dim3(rows), dim3(NT), 0, (hipStream_t)stream, (const half_t*)x, w, (half_t*)y, rows, D, L, H, sb, sh,
-                       sl, eps, nullptr, 0L);
-    return (int)hipGetLastError();
+    // Chunks per thread: as many as D needs (the loads of a thread's unused chunks are not free).
+    auto launch = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3(rows), dim3(NT), 0, (hipStream_t)stream, (const half_t*)x, w, (half_t*)y, rows, D, L, H, sb, sh, sl, eps, nullptr,
+                           0L);
+        return (int)hipGetLastError();
+    };
+    switch ((D / 8 + NT - 1) / NT) {
+    case 1: return launch(norm_kernel<NT, 1, false>);
+    case 2: return launch(norm_kernel<NT, 2, false>);
+    case 3: return launch(norm_kernel<NT, 3, false>);
+    default: return launch(norm_kernel<NT, 4, false>);
+    }
 }
 
 // rms_norm_rope (rms_norm.hip:75-77): QK-norm over D = 128 then RoPE; freqs [.., L, 64, 2, 2] fp32,
