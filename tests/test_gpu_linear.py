@@ -56,6 +56,24 @@ def test_activation_rot_quant_bit_exact(dev, act, M, K, group):
     assert_same(q_of(packed, M, K), q_ref)
 
 
+def test_swiglu_every_fp16_gate(dev):
+    """Every finite fp16 gate value through the SwiGLU kernel (whose silu takes a fast path away from fp16 rounding
+    midpoints): row r has gate g_r at element 0 and 0 elsewhere, up = 16 there (1 where |g| > 2048, so the product
+    stays finite) and 1 elsewhere. The rotated row is then +-r16(silu(g_r)) up / 16 in every element, exactly, so
+    the row scale fixes |r16(silu(g_r))| and the codes its sign."""
+    g = np.arange(65536, dtype=np.uint16).view(np.float16)
+    g = g[np.isfinite(g)]
+    M, K = len(g), 256
+    gate = np.zeros((M, K), np.float16)
+    gate[:, 0] = g
+    up = np.ones((M, K), np.float16)
+    up[:, 0] = np.where(np.abs(g) <= 2048, 16, 1)
+    packed, scale = int8_gemm.quantize(kern().swiglu_rot_quant_pack_a, torch.from_numpy(gate).to(dev), K, up=torch.from_numpy(up).to(dev), group=256)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(gate, act=oracle.ACT_SWIGLU, group=256, u=up)
+    assert_same(scale.cpu().numpy(), s_ref)
+    assert_same(q_of(packed, M, K), q_ref)
+
+
 @pytest.mark.parametrize("B,L,K", [(1, 77, 3072), (2, 40, 1024)])
 def test_mod_rot_quant_bit_exact(dev, B, L, K):
     print(f"mod_rot_quant B={B} L={L} K={K}", flush=True)
