@@ -6,8 +6,9 @@ timed steps (4 B H S^2 D = 206.16 GFLOP per step). The other configurations of t
 GEMM TOPS), int8-QK attention, the W4A8 linear, the DiT MLP tail and the decode GEMV / attention (HBM GB/s) -- are
 measured in the same run and reported under "components".
 
-Timing: the timed steps run back to back between two HIP events on torch's current stream (the stream the
-library launches on); `roofline.achieved` = algorithmic work / mean time per step. Kernels shorter than ~50 us are timed by replaying a
+Timing: each workload first runs untimed for 50 ms (the shader clock needs ~20-25 ms of load to leave its idle
+state), then its warm-up steps; the timed steps run back to back between two HIP events on torch's current stream
+(the stream the library launches on); `roofline.achieved` = algorithmic work / mean time per step. Kernels shorter than ~50 us are timed by replaying a
 captured HIP graph of many launches, so host launch overhead does not stretch them. HBM-bound kernels rotate over
 more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve them. The CPU baseline is the
 reference's attention fallback (attention_bmm: chunked baddbmm -> softmax -> bmm, attention.py:15-43) on the host
@@ -55,9 +56,27 @@ def gen(torch, seed):
     return torch.Generator().manual_seed(seed)
 
 
+SPIN_UP_S = 0.05  # untimed work before the warm-up steps: the shader clock needs ~20-25 ms of load to leave idle
+
+
+def spin_up(torch, fn, copies=1, seconds=SPIN_UP_S):
+    """Runs fn(i) untimed until `seconds` of wall time have passed with the GPU busy. After an idle spell (inputs
+    built on the host, the previous workload's bookkeeping) the shader clock ramps up over ~20-25 ms of load: the
+    fp16 attention's first calls take ~2x, its first 60 ~1.1x the steady time. Without this a short timed region
+    measures the ramp, not the kernel."""
+    torch.cuda.synchronize()
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn(i % copies)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def event_timed(torch, fn, steps, warmup, copies=1):
     """warmup + steps calls of fn(i), back to back; returns (wall ms per step, ms per step between two HIP events
     recorded on torch's current stream -- the stream the library launches on -- around the timed region)."""
+    spin_up(torch, fn, copies)
     for i in range(warmup):
         fn(i % copies)
     torch.cuda.synchronize()
@@ -75,6 +94,7 @@ def event_timed(torch, fn, steps, warmup, copies=1):
 def graph_timed(torch, fn, steps, warmup, copies=1):
     """Captures GRAPH_LAUNCHES calls of fn(i) (cycling over the copies) in one HIP graph and replays it; returns
     (ms per call over the replays, same) -- back-to-back launches without host overhead."""
+    spin_up(torch, fn, copies)
     for i in range(max(warmup, 2)):
         fn(i % copies)
     torch.cuda.synchronize()

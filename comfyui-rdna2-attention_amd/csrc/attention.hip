@@ -187,13 +187,38 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         }
     };
 
-    // S^T of the tile in stage st (scaled for int8), into s.
+    // LDS offsets of the lane's V^T reads (and int8 K reads) within a stage, fixed for the whole loop: the stage
+    // enters as an immediate offset (the loop below is unrolled over the two stages), so the tile loop spends
+    // no VALU on them. Kept opaque so that the compiler holds them in VGPRs rather than recomputing them.
+    u32 k_rd[4], v_rd[4];
+    u32 ks_rd = 0;
+    if (I8) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) k_rd[ks] = (u32)(lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+        ks_rd = (u32)(KB * 128 + 16 * g);
+        asm volatile("" : "+v"(ks_rd));
+    }
+    {
+        const int sg = lane & 15;
+        const u32 vt = (u32)(T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
+        const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) v_rd[dt] = vt + (u32)(((4 * dt) ^ vx) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (I8) asm volatile("" : "+v"(k_rd[i]));
+#pragma unroll
+    for (int i = 0; i < 4; i++) asm volatile("" : "+v"(v_rd[i]));
+
+    // S^T of the tile in stage ST (scaled for int8), into s.
     float s[16];
-    auto scores = [&](const char* st) {
+    auto scores = [&](auto stage) __attribute__((always_inline)) {
+        const char* st = smem + decltype(stage)::value * T::BYTES;
         if (!I8) {
             // K operands in two batches of four reads; each batch goes out before the products that use it.
-            // Lane-dependent parts of the addresses are recomputed here from an opaque copy of the lane id:
-            // hoisted out of the tile loop they would hold VGPRs for its whole length.
+            // Their addresses are recomputed per tile from an opaque copy of the lane id: eight more VGPRs held
+            // across the loop would spill.
             int ln = lane;
             asm volatile("" : "+v"(ln));
             const char* krow = st + (ln & 31) * 256;
@@ -212,17 +237,16 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 #pragma unroll
             for (int r = 0; r < 16; r++) s[r] = acc[r];
         } else {
-            const float* kscale = (const float*)(st + KB * 128);
             i4v ka[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(st + lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(st + k_rd[ks]);
             __builtin_amdgcn_sched_barrier(0);
             i16v acc = {};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++) {
-                const f4 sc = *(const f4*)(kscale + 8 * r4 + 4 * g);
+                const f4 sc = *(const f4*)(st + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
 #pragma unroll
                 for (int e = 0; e < 4; e++) s[r4 * 4 + e] = (float)acc[r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
             }
@@ -261,18 +285,14 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             pf[r >> 3][(r & 7) + 1] = pk[1];
         }
     };
-    // O^T += V^T P^T with the V tile in vst and P in pf; the second step's V^T operands are read while the
+    // O^T += V^T P^T with the V tile of stage ST and P in pf; the second step's V^T operands are read while the
     // first step's products run.
-    auto pv = [&](const char* vst) {
-        int ln = lane;  // opaque lane id, as in scores
-        asm volatile("" : "+v"(ln));
-        const int sg = ln & 15;
-        const char* vt = vst + (4 * (ln >> 5) + (sg >> 2)) * 256 + (sg & 1) * 8;
-        const int vx = (2 * ((ln >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
-        auto read_v = [&](h8 (&va)[4], int j) {
+    auto pv = [&](auto stage) __attribute__((always_inline)) {
+        const char* st = smem + decltype(stage)::value * T::BYTES;
+        auto read_v = [&](h8 (&va)[4], int j) __attribute__((always_inline)) {
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) {
-                const char* ra = vt + 16 * j * 256 + (((4 * dt) ^ vx) << 4);
+                const char* ra = st + v_rd[dt] + 16 * j * 256;
                 va[dt] = __builtin_shufflevector(read_tr(ra), read_tr(ra + 8 * 256), 0, 1, 2, 3, 4, 5, 6, 7);
             }
         };
@@ -287,24 +307,39 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     };
 
     // Tile loop: the copies of tile i + 1 go out before the work on tile i and are awaited at its closing
-    // barrier, which also retires every read of the stage the next copies overwrite. The last tile -- the
-    // only one that can reach past Lk -- is peeled off with the masking (under a runtime test the compiler
-    // turns the masking into selects on every tile).
-    auto stage = [&](int i) -> const char* { return smem + (i & 1) * T::BYTES; };
-    issue(0, stage(0));
-    wait_copies();
-    __syncthreads();
-    for (int i = 0; i < tiles - 1; i++) {
-        issue((i + 1) * KB, stage(i + 1));
-        scores(stage(i));
-        softmax(i * KB, std::false_type{});
-        pv(stage(i) + T::K_BYTES);
+    // barrier, which also retires every read of the stage the next copies overwrite. Unrolled over the two
+    // stages. The last tile -- the only one that can reach past Lk -- is peeled off with the masking (under a
+    // runtime test the compiler turns the masking into selects on every tile).
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    auto tile = [&](int i, auto stage, auto last) __attribute__((always_inline)) {
+        if constexpr (!decltype(last)::value) issue((i + 1) * KB, smem + (decltype(stage)::value ^ 1) * T::BYTES);
+        scores(stage);
+        softmax(i * KB, last);
+        pv(stage);
+        if constexpr (!decltype(last)::value) {
+            wait_copies();
+            __syncthreads();
+        }
+    };
+    // Tile i uses stage (tiles - 1 - i) & 1, so the last tile is always in stage 0 and the loop runs in whole pairs.
+    int i = 0;
+    if (tiles % 2 == 0) {
+        issue(0, smem + T::BYTES);
+        wait_copies();
+        __syncthreads();
+        tile(0, S1{}, std::false_type{});
+        i = 1;
+    } else {
+        issue(0, smem);
         wait_copies();
         __syncthreads();
     }
-    scores(stage(tiles - 1));
-    softmax((tiles - 1) * KB, std::true_type{});
-    pv(stage(tiles - 1) + T::K_BYTES);
+    for (; i < tiles - 1; i += 2) {
+        tile(i, S0{}, std::false_type{});
+        tile(i + 1, S1{}, std::false_type{});
+    }
+    tile(tiles - 1, S0{}, std::true_type{});
 
     // Normalise and store: the lane halves hold disjoint keys of one row.
     const f2 lh = halves(l);

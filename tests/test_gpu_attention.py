@@ -34,7 +34,8 @@ def close(out, ref):
 
 
 @pytest.mark.parametrize("int8_qk", [False, True])
-@pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096)])
+@pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096),
+                                          (1, 2, 1, 200, 1049), (1, 1, 1, 64, 96)])
 def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
     print(f"attention B={B} H={H} Hkv={Hkv} Lq={Lq} Lk={Lk} int8_qk={int8_qk}", flush=True)
     q, k, v = qkv(B, H, Hkv, Lq, Lk, seed=Lq + Lk)
