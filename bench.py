@@ -16,6 +16,8 @@ cores over a bounded sample.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME]
 
+"dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192, 4096 tokens).
+
 `--only NAME` runs one workload (the names of "components", "attention_f16", or "copy": a 1 GiB device copy used to
 calibrate FETCH_SIZE / WRITE_SIZE) and prints its line; the rocprofv3 summaries in profiles/ are made that way.
 """
@@ -57,20 +59,21 @@ def gen(torch, seed):
 
 
 SPIN_UP_S = 0.05  # untimed work before the warm-up steps: the shader clock needs ~20-25 ms of load to leave idle
+SPIN_UP_CALLS = 100
 
 
-def spin_up(torch, fn, copies=1, seconds=SPIN_UP_S):
-    """Runs fn(i) untimed until `seconds` of wall time have passed with the GPU busy. After an idle spell (inputs
-    built on the host, the previous workload's bookkeeping) the shader clock ramps up over ~20-25 ms of load: the
-    fp16 attention's first calls take ~2x, its first 60 ~1.1x the steady time. Without this a short timed region
-    measures the ramp, not the kernel."""
+def spin_up(torch, fn, copies=1, seconds=SPIN_UP_S, calls=SPIN_UP_CALLS):
+    """Runs fn(i) untimed, back to back, for at least `calls` calls and `seconds` of host time, then waits for them.
+    After an idle spell (inputs built on the host) the shader clock ramps up over ~20-25 ms of load: the fp16
+    attention's first calls take ~2x, its first 60 ~1.1x the steady time. The calls are not interleaved with
+    synchronisations: with them, the fused block's first ~100 calls after setup ran ~1.7x slower than later ones
+    (host-bound: the host's own enqueue rate recovers only under continuous load)."""
     torch.cuda.synchronize()
     t0, i = time.perf_counter(), 0
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(8):
-            fn(i % copies)
-            i += 1
-        torch.cuda.synchronize()
+    while i < calls or time.perf_counter() - t0 < seconds:
+        fn(i % copies)
+        i += 1
+    torch.cuda.synchronize()
 
 
 def event_timed(torch, fn, steps, warmup, copies=1):
@@ -263,6 +266,32 @@ def w_decode_attention(torch, dev):
     return fn, len(kv), 2 * cap * Hkv * 512 + 2 * H * 512, "hbm", graph_timed
 
 
+def w_dit_block(torch, dev):
+    """The fused Krea 2 block, int8_gemm.block_forward, at the DiT size: hidden 3072 (24 heads x 128), MLP 8192, 4096
+    tokens, B=1, fp16 attention -- driven through int8_gemm's hooks over the stand-in INT8-Fast-ROCM layers of
+    tests/fakes.py (ComfyUI and the plugin are not installed here), int8 weights uniform in [-127, 127]. Work, in
+    int8-equivalent ops: its eight GEMMs (5 x 2 * 4096 * 3072^2 + 3 x 2 * 4096 * 3072 * 8192 = 1005.3 G) plus the
+    attention's 206.2 GFLOP counted twice (the fp16 matrix peak is half the int8 one); the roofline is the int8
+    peak, so its fraction is the all-MFMA time over the block's time."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import fakes
+    from comfyui_rdna2_attention_amd import int8_gemm, rms_norm
+    sys.modules.update(fakes.make_pack(real=True))
+    int8_gemm.comfy = rms_norm.comfy = fakes.make_comfy()
+    int8_gemm.originals.clear()
+    int8_gemm.enable(True)
+    L, D, H, hidden = 4096, 3072, 24, 8192
+    blk = fakes.make_krea2_block(sys.modules["fakepack.int8_quant"].Int8TensorwiseOps.Linear, D, H, hidden, 1, dev, seed=20)
+    x = torch.randn(1, L, D, generator=gen(torch, 21)).half().to(dev)
+    ang = torch.randn(1, 1, L, 64, generator=gen(torch, 22))
+    freqs = torch.stack([torch.cos(ang), -torch.sin(ang), torch.sin(ang), torch.cos(ang)], -1).reshape(1, 1, L, 64, 2, 2).float().to(dev)
+    out = int8_gemm.block_forward(blk, False, x, None, freqs)
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError("dit_block: non-finite block output")
+    work = 5 * 2.0 * L * D * D + 3 * 2.0 * L * D * hidden + 2 * ATTN_FLOP
+    return (lambda i: int8_gemm.block_forward(blk, False, x, None, freqs)), 1, work, "mfma_i8", event_timed
+
+
 def w_copy(torch, dev):
     """An elementwise kernel that reads 1 GiB and writes 1 GiB (torch.neg on fp32): the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters."""
@@ -285,6 +314,7 @@ WORKLOADS = {
     "decode_gemv_n1024": lambda t, d: w_decode_gemv(t, d, 1024),
     "decode_gemv_n12288": lambda t, d: w_decode_gemv(t, d, 12288),
     "decode_attention": w_decode_attention,
+    "dit_block": w_dit_block,  # last: it installs the hooks over stand-in plugin modules for the rest of the run
     "copy": w_copy,
 }
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}

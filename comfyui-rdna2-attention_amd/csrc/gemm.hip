@@ -337,21 +337,48 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
                 }
             }
     };
+    constexpr int ITER = BM * CPR / GT;  // 16-byte chunks per thread (the tile is a whole number of them)
+    static_assert(BM * CPR % GT == 0, "whole chunks per thread");
+    if (!R) {
+        if (bias) dequantize(std::integral_constant<bool, true>{});
+        else dequantize(std::integral_constant<bool, false>{});
+        __syncthreads();
+#pragma unroll 4
+        for (int it = 0; it < ITER; it++) {
+            const int idx = t + it * GT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
+            if (m < M) *(h8*)(C + (size_t)m * N + n0 + c) = *(const h8*)(tile + r * TP + c * 2);
+        }
+        return;
+    }
+    // Gated residual: R and G are read in batches of RB chunks per thread, double-buffered, with row indices
+    // clamped in bounds so that no load sits under a branch; the first batch goes out before the dequantization
+    // pass, whose LDS work then covers its latency. (One load per chunk, each awaited before its store, left
+    // the epilogue latency-bound: +17 us on 4096 x 3072 x 3072.)
+    constexpr int RB = ITER % 8 == 0 ? 8 : ITER % 4 == 0 ? 4 : 1, NBATCH = ITER / RB;
+    h8 res[2][RB], gat[2][RB];
+    auto load = [&](int b, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < RB; k++) {
+            const int idx = t + (b * RB + k) * GT, r = idx / CPR, c = (idx % CPR) * 8, m = min(m0 + r, M - 1);
+            res[slot][k] = *(const h8*)(R + (size_t)m * N + n0 + c);
+            gat[slot][k] = *(const h8*)(G + (size_t)(m / L) * N + n0 + c);
+        }
+    };
+    load(0, 0);
     if (bias) dequantize(std::integral_constant<bool, true>{});
     else dequantize(std::integral_constant<bool, false>{});
     __syncthreads();
-#pragma unroll 4
-    for (int idx = t; idx < BM * CPR; idx += GT) {
-        const int r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
-        if (m >= M) continue;
-        h8 y = *(const h8*)(tile + r * TP + c * 2);
-        const size_t at = (size_t)m * N + n0 + c;
-        if (R) {
-            const h8 res = *(const h8*)(R + at), gate = *(const h8*)(G + (size_t)(m / L) * N + n0 + c);
 #pragma unroll
-            for (int e = 0; e < 8; e++) y[e] = to_half((float)res[e] + r16((float)gate[e] * (float)y[e]));
+    for (int b = 0; b < NBATCH; b++) {
+        if (b + 1 < NBATCH) load(b + 1, (b + 1) & 1);
+#pragma unroll
+        for (int k = 0; k < RB; k++) {
+            const int idx = t + (b * RB + k) * GT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
+            h8 y = *(const h8*)(tile + r * TP + c * 2);
+#pragma unroll
+            for (int e = 0; e < 8; e++) y[e] = to_half((float)res[b & 1][k][e] + r16((float)gat[b & 1][k][e] * (float)y[e]));
+            if (m < M) *(h8*)(C + (size_t)m * N + n0 + c) = y;
         }
-        *(h8*)(C + at) = y;
     }
 }
 

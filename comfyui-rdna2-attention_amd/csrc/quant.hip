@@ -52,9 +52,12 @@ __device__ __forceinline__ float situ(float hidden, float gate) {
 // silu by a fast path: hardware exp2 of a rounded argument and a hardware reciprocal. Over every fp16 g whose
 // silu is an fp16 normal number the fast value is within 11 fp32 ulps of the exact one (measured on all 65536
 // inputs: <= 4 ulps for |g| < 4), so where it lies more than SILU_T ulps from an fp16 rounding midpoint both
-// round to the same fp16 value. Values that are not (about 0.3% of inputs, and every result outside
-// [2^-14, 2^15) or not finite) take the exact formula; the SwiGLU tests compare all 65536 fp16 gates with the
-// oracle through the kernel.
+// round to the same fp16 value. Below 2^-14 (g < about -12) the results fall on fp16's subnormal grid, whose
+// spacing 2^-24 continues that of the lowest normal binade: there the test is the distance of |q| 2^24 from
+// the nearest half-integer, again against SILU_T ulps (silu_sure_tiny; the fast value's error stays within the
+// same bound there, and the tiny values that round to zero are sure by the same test). Values that pass neither
+// (about 0.3% of inputs, and results from 2^15 up or not finite) take the exact formula; the SwiGLU tests
+// compare all 65536 fp16 gates with the oracle through the kernel.
 #define SILU_T 12
 __device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
 __device__ __forceinline__ bool silu_sure(float q) {
@@ -62,6 +65,12 @@ __device__ __forceinline__ bool silu_sure(float q) {
     const bool mid = ((__float_as_uint(q) + (SILU_T - 0x1000)) & 0x1fffu) <= 2 * SILU_T;
     const float a = fabsf(q);
     return !mid && a >= __uint_as_float(0x38800040u) && a < 32768.f;
+}
+__device__ __forceinline__ bool silu_sure_tiny(float q) {
+    const float r = fabsf(q) * 16777216.f;  // exact: |q| in units of the fp16 grid spacing 2^-24
+    const float f = r - floorf(r);          // exact
+    const float ulp = __uint_as_float(__float_as_uint(r) & 0x7f800000u) * (1.f / 8388608.f);
+    return r < 1024.f && fabsf(f - 0.5f) > SILU_T * ulp;
 }
 // int8_gemm.hip:135-137
 __device__ __forceinline__ float sigmoid_gate(float x, float gate) { return r16(x * r16(1.f / (1.f + rda_expf(-gate)))); }
@@ -158,13 +167,17 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
                         sg[i] = silu_fast((float)(i < 8 ? lo[i] : hi[i - 8]));
                         unsure[i] = !silu_sure(sg[i]);
                     }
-                    // The exact formula, for the positions where some lane of the wave is unsure.
+                    // For the positions where some lane of the wave is unsure: the subnormal-range test, then the exact
+                    // formula where that does not settle it either.
 #pragma unroll
                     for (int i = 0; i < 16; i++) {
                         if (__any(unsure[i])) {
-                            const float gi = (float)(i < 8 ? lo[i] : hi[i - 8]);
-                            const float exact = gi / (1.f + rda_expf(-gi));
-                            if (unsure[i]) sg[i] = exact;
+                            unsure[i] = unsure[i] && !silu_sure_tiny(sg[i]);
+                            if (__any(unsure[i])) {
+                                const float gi = (float)(i < 8 ? lo[i] : hi[i - 8]);
+                                const float exact = gi / (1.f + rda_expf(-gi));
+                                if (unsure[i]) sg[i] = exact;
+                            }
                         }
                     }
 #pragma unroll

@@ -142,8 +142,9 @@ def test_w8a8_linear_bit_exact(dev, M, N, K, group, bias):
     assert_same(bits(out), bits(ref))
 
 
-def test_gemm_residual_epilogue_bit_exact(dev):
-    B, L, K, N = 2, 300, 512, 256
+@pytest.mark.parametrize("B,L,K,N", [(2, 300, 512, 256), (1, 600, 256, 576), (2, 2048, 256, 8192)])  # 128-, 192- and 256-wide tiles
+def test_gemm_residual_epilogue_bit_exact(dev, B, L, K, N):
+    print(f"residual epilogue B={B} L={L} K={K} N={N}", flush=True)
     M = B * L
     g = gen(9)
     x = activations(M, K, seed=7)
