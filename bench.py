@@ -6,8 +6,8 @@ timed steps (4 B H S^2 D = 206.16 GFLOP per step). The other configurations of t
 GEMM TOPS), int8-QK attention, the W4A8 linear, the DiT MLP tail and the decode GEMV / attention (HBM GB/s) -- are
 measured in the same run and reported under "components".
 
-Timing: each workload first runs untimed for 50 ms (the shader clock needs ~20-25 ms of load to leave its idle
-state), then its warm-up steps; the timed steps run back to back between two HIP events on torch's current stream
+Timing: each workload first runs untimed, back to back, for at least 50 ms and 100 calls (the shader clock needs
+~20-25 ms of load to leave its idle state), then its warm-up steps; the timed steps run back to back between two HIP events on torch's current stream
 (the stream the library launches on); `roofline.achieved` = algorithmic work / mean time per step. Kernels shorter than ~50 us are timed by replaying a
 captured HIP graph of many launches, so host launch overhead does not stretch them. HBM-bound kernels rotate over
 more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve them. The CPU baseline is the
@@ -16,6 +16,7 @@ cores over a bounded sample.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME]
 
+"decode_layer" times one token through one Qwen3-8B-shaped layer's int8 linears and decode attention, and
 "dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192, 4096 tokens).
 
 `--only NAME` runs one workload (the names of "components", "attention_f16", or "copy": a 1 GiB device copy used to
@@ -266,6 +267,49 @@ def w_decode_attention(torch, dev):
     return fn, len(kv), 2 * cap * Hkv * 512 + 2 * H * 512, "hbm", graph_timed
 
 
+def w_decode_layer(torch, dev):
+    """One token through one Qwen3-8B-shaped layer as int8_gemv's patched forwards run it (int8_gemv.py:48-64,
+    111-113): hidden 4096, 32 query / 8 KV heads of 128, MLP 12288, KV cache length 2048 (fp32). Each of the seven
+    int8 linears is linear_forward's single-token path -- ConvRot of its fp32 input (group 256, int8_gemv.rotate)
+    then the GEMV (int8_gemv.gemv) -- and attention is int8_gemv.attention_decode; the layer's own torch ops (norms,
+    rope, silu * up, residual adds) are outside this path and not included. Replayed from a HIP graph, as a decode
+    loop would, over enough weight and cache copies that the Infinity Cache cannot serve them. Bytes: the int8
+    weights, their scales, the K/V cache and the activations read and written."""
+    from comfyui_rdna2_attention_amd import int8_gemv
+    D, Hq, Hkv, F, cap = 4096, 32, 8, 12288, 2048
+    shapes = {"q": (D, D), "k": (Hkv * 128, D), "v": (Hkv * 128, D), "o": (D, D), "gate": (F, D), "up": (F, D), "down": (D, F)}
+    weights_bytes = sum(n * k for n, k in shapes.values())
+    kv_bytes = 2 * cap * Hkv * 128 * 4
+    copies = max(1, ROTATE_BYTES // (weights_bytes + kv_bytes) + 1)
+    g = gen(torch, 40)
+    layers = []
+    for _ in range(copies):
+        w = {name: torch.randint(-127, 128, shp, generator=g, dtype=torch.int8).to(dev) for name, shp in shapes.items()}
+        s = {name: (torch.rand(shp[0], generator=g) * 2e-3 + 1e-3).float().to(dev) for name, shp in shapes.items()}
+        kv = [torch.randn(1, cap, Hkv, 128, generator=g).float().to(dev) for _ in range(2)]
+        layers.append((w, s, kv))
+    x = torch.randn(1, 1, D, generator=g).float().to(dev)
+    lengths = torch.full((1,), cap, dtype=torch.int32, device=dev)
+
+    def lin(name, w, s, inp):
+        return int8_gemv.gemv(int8_gemv.rotate(inp, 256), w[name], s[name])
+
+    def step(i):
+        w, s, (kc, vc) = layers[i]
+        q = lin("q", w, s, x)
+        lin("k", w, s, x)
+        lin("v", w, s, x)
+        o = int8_gemv.attention_decode(q.view(1, 1, Hq, 128), kc, vc, lengths)
+        h = lin("o", w, s, o.view(1, 1, D))
+        gate = lin("gate", w, s, h)
+        lin("up", w, s, h)
+        return lin("down", w, s, gate)
+
+    act = 4 * (D * 10 + Hkv * 128 * 2 + F * 4)  # fp32 inputs read (7 rotations, 7 GEMVs) and outputs written, roughly
+    work = weights_bytes + 4 * sum(n for n, _ in shapes.values()) + kv_bytes + act
+    return step, copies, work, "hbm", graph_timed
+
+
 def w_dit_block(torch, dev):
     """The fused Krea 2 block, int8_gemm.block_forward, at the DiT size: hidden 3072 (24 heads x 128), MLP 8192, 4096
     tokens, B=1, fp16 attention -- driven through int8_gemm's hooks over the stand-in INT8-Fast-ROCM layers of
@@ -314,6 +358,7 @@ WORKLOADS = {
     "decode_gemv_n1024": lambda t, d: w_decode_gemv(t, d, 1024),
     "decode_gemv_n12288": lambda t, d: w_decode_gemv(t, d, 12288),
     "decode_attention": w_decode_attention,
+    "decode_layer": w_decode_layer,
     "dit_block": w_dit_block,  # last: it installs the hooks over stand-in plugin modules for the rest of the run
     "copy": w_copy,
 }

@@ -2,6 +2,7 @@
 predicates and fallbacks to the original functions, state reset, and that an eligible call never computes on the
 CPU (it raises without a GPU). ComfyUI and ComfyUI-INT8-Fast-ROCM are replaced by the stand-ins of tests/fakes.py."""
 import logging
+import types
 
 import numpy as np
 import pytest
@@ -289,3 +290,19 @@ def test_launch_shim_ignores_reference_grid():
     assert list(inspect.signature(hip_attention.launch).parameters) == ["func", "grid_x", "grid_y", "block", "args", "shared"]
     with pytest.raises(RuntimeError, match="HIP error 7"):
         hip_attention.check(7)
+
+
+def test_init_kv_cache_layout(monkeypatch):
+    """init_kv_cache (int8_gemv.py:117-126): one fixed-capacity (batch, capacity, kv heads, 128) K and V per layer,
+    all layers sharing the position and the int32 length tensors that the decode kernels read on the device."""
+    import collections
+    FixedKV = collections.namedtuple("FixedKV", "key value index position length")
+    monkeypatch.setattr(int8_gemv, "FixedKV", FixedKV)
+    model = types.SimpleNamespace(config=types.SimpleNamespace(num_hidden_layers=3, num_key_value_heads=8))
+    caches = int8_gemv.init_kv_cache(model, 2, 64, torch.device("cpu"), torch.float32)
+    assert len(caches) == 3
+    for c in caches:
+        assert c.key.shape == c.value.shape == (2, 64, 8, 128) and c.key.dtype == torch.float32 and c.index == 0
+        assert c.key.data_ptr() != c.value.data_ptr()
+        assert c.position is caches[0].position and c.length is caches[0].length
+    assert caches[0].length.dtype == torch.int32 and int(caches[0].length.abs().sum()) == 0

@@ -1,0 +1,107 @@
+"""The text-generation path around the decode kernels (int8_gemv.py:48-126) on the GPU: linear_forward's single-token
+GEMV with and without the ConvRot of its input, the bf16 logits of the last position, and a decode attention step
+captured once in a HIP graph and replayed as the cache grows. ComfyUI's quantized-weight context
+(comfy.ops.CastBiasWeightContext) is stood in for: it hands the layer's int8 weight (`_qdata`, `_params.scale`) and
+bias to the code under test, which is all the patched forwards read from it.
+
+Bounds: the GEMVs as in test_gpu_decode_norm (|out - ref| <= 1e-5 * scale * sum_k |w x| against float64; the rotation
+is bit-exact, so the GEMV sees the oracle's rotated input); decode attention |out - ref| <= 1e-5 + 1e-4 |ref|, and
+every graph replay equal bit for bit to an eager call at the same length."""
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from comfyui_rdna2_attention_amd import int8_gemv
+from helpers import channel_scales, gen, int8_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def stand_in_comfy(monkeypatch, pairs):
+    """comfy.ops.CastBiasWeightContext yielding pairs[id(module)] = (weight, bias) for the module it is given."""
+    class CastBiasWeightContext:
+        def __init__(self, module, **kwargs):
+            self.pair = pairs[id(module)]
+
+        def __enter__(self):
+            return self.pair
+
+        def __exit__(self, *exc):
+            return False
+
+    monkeypatch.setattr(int8_gemv, "comfy", types.SimpleNamespace(ops=types.SimpleNamespace(CastBiasWeightContext=CastBiasWeightContext)))
+
+
+def int8_layer():
+    layer = types.SimpleNamespace(weight_function=[], bias_function=[])
+    layer.forward = None  # never reached on the single-token path
+    return layer
+
+
+@pytest.mark.parametrize("group", [0, 256, 1024])
+@pytest.mark.parametrize("N,K,bias", [(1024, 4096, False), (4096, 4096, True), (512, 12288, False)])
+def test_linear_forward_single_token(dev, monkeypatch, N, K, bias, group):
+    print(f"linear_forward N={N} K={K} bias={bias} group={group}", flush=True)
+    w = int8_weights(N, K, seed=30)
+    s = channel_scales(N, seed=31)
+    b = torch.randn(N, generator=gen(32)).float() if bias else None
+    layer = int8_layer()
+    weight = types.SimpleNamespace(_qdata=w.to(dev), _params=types.SimpleNamespace(scale=s.to(dev)))
+    stand_in_comfy(monkeypatch, {id(layer): (weight, None if b is None else b.to(dev))})
+    x = torch.randn(1, 1, K, generator=gen(33)).float()
+    out = int8_gemv.linear_forward(layer, N, K, torch.int8, group, x.to(dev))
+    assert out.shape == (1, 1, N) and out.dtype == torch.float32
+    xr = oracle.rotate_f32(x.numpy().reshape(1, K), group).reshape(-1) if group else x.numpy().reshape(-1)
+    ref = oracle.gemv_f64(xr, w.numpy(), s.numpy(), None if b is None else b.numpy())
+    bound = 1e-5 * (np.abs(w.numpy().astype(np.float64)) @ np.abs(xr.astype(np.float64))) * np.abs(s.numpy()) + 1e-12
+    err = np.abs(out.cpu().double().numpy().reshape(-1) - ref)
+    assert np.all(err <= bound), f"max err {err.max():.3e}"
+
+
+def test_logits_of_the_last_position(dev, monkeypatch):
+    N, K, L = 4096, 2560, 7
+    table = torch.randn(N, K, generator=gen(34)).bfloat16()
+    embed = types.SimpleNamespace(weight_function=[])
+    transformer = types.SimpleNamespace(model=types.SimpleNamespace(embed_tokens=embed))
+    stand_in_comfy(monkeypatch, {id(embed): (table.to(dev), None)})
+    x = torch.randn(1, L, K, generator=gen(35)).float()
+    out = int8_gemv.logits(transformer, x.to(dev))
+    assert out.shape == (1, 1, N) and out.dtype == torch.float32
+    wd, xd = table.double().numpy(), x[0, -1].double().numpy()
+    ref = wd @ xd
+    bound = 1e-5 * (np.abs(wd) @ np.abs(xd))
+    assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - ref) <= bound)
+
+
+def test_decode_step_graph_replays_as_the_cache_grows(dev):
+    """One capture, replays at growing lengths (the length is read on the device, int8_gemv.py:117-126); eager work
+    between the replays, each replay checked against an eager call and the float64 restatement."""
+    B, H, Hkv, cap = 1, 32, 8, 2048
+    g = gen(36)
+    q = torch.randn(B, 1, H, 128, generator=g).float().to(dev)
+    k = torch.randn(B, cap, Hkv, 128, generator=g).float().to(dev)
+    v = torch.randn(B, cap, Hkv, 128, generator=g).float().to(dev)
+    lengths = torch.ones(B, dtype=torch.int32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        int8_gemv.attention_decode(q, k, v, lengths)  # warm-up on the capture stream
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            out = int8_gemv.attention_decode(q, k, v, lengths)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for L in (1, 33, 700, 2047, 2048, 5):
+        print(f"graph replay at length {L}", flush=True)
+        lengths.fill_(L)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = int8_gemv.attention_decode(q, k, v, lengths)
+        assert torch.equal(out, eager)
+        ref = oracle.attention_decode_f64(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), [L])
+        err = np.abs(out.cpu().double().numpy() - ref)
+        assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"length {L}: max err {err.max():.3e}"
+
