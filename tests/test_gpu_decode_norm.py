@@ -15,11 +15,20 @@ from helpers import assert_same, bits, channel_scales, gen, int8_weights
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("rows,group", [(1, 256), (3, 1024), (2, 64), (1, 16384), (5, 16)])
+@pytest.mark.parametrize("rows,group", [(1, 256), (3, 1024), (2, 64), (1, 16384), (5, 16), (7, 4), (16, 256), (48, 256), (3, 64), (13, 16)])
 def test_rotate_bit_exact(dev, rows, group):
     x = torch.randn(rows, group, generator=gen(group)).float()
     out = int8_gemv.rotate(x.to(dev), group)
     assert_same(out.cpu().numpy(), oracle.rotate_f32(x.numpy(), group))
+
+
+def test_rotate_unaligned_view(dev):
+    """A contiguous view that starts 4 bytes into its storage: same values as the oracle's rotation."""
+    base = torch.randn(1 + 4096, generator=gen(41)).float().to(dev)
+    x = base[1:].view(1, 4096)
+    assert x.is_contiguous() and x.data_ptr() % 16 != 0
+    out = int8_gemv.rotate(x, 256)
+    assert_same(out.cpu().numpy(), oracle.rotate_f32(x.cpu().numpy().reshape(16, 256), 256).reshape(1, 4096))
 
 
 def gemv_bound(w, x, scale, half):
