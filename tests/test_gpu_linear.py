@@ -108,7 +108,8 @@ def packed_from(a_int8):
     return torch.from_numpy(np.ascontiguousarray(a_int8)).view(torch.int32).reshape(-1)
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 3072, 3072), (1000, 192, 512), (513, 64, 64), (256, 256, 8192), (77, 128, 1024), (300, 320, 192)])
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 3072), (1000, 192, 512), (513, 64, 64), (256, 256, 8192), (77, 128, 1024), (300, 320, 192),
+                                   (512, 3072, 6144)])  # the last: the shape of the reference's gemm_k6144 (int8_gemm.hip:414)
 def test_gemm_int32_accumulators_exact(dev, M, N, K):
     print(f"gemm_acc M={M} N={N} K={K}", flush=True)
     g = gen(M + N + K)
