@@ -406,7 +406,7 @@ def cpu_baseline(torch, q, k, v, seconds=10.0):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
+        print(f"bench.py measures one GPU: there is no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -1,7 +1,7 @@
 """CPU oracle for the quantized-inference hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
-leg import this package, and only as the checker or the timed CPU baseline. The
+leg import this package, and only as the reference results or the timed CPU baseline. The
 product path (the package ``comfyui-rdna2-attention_amd``) never imports it.
 
 Two halves:

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the quantized-inference hot path. TEST INFRASTRUCTURE ONLY:
  * the tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this
- * library as the checker. The product path never links or calls it.
+ * library as the source of reference results. The product path never links or calls it.
  *
  * Every function restates, operation by operation, the arithmetic that the
  * reference kernels perform (citations are file:line in the reference repo),
@@ -328,7 +328,7 @@ void orc_gemm_epilogue(int M, int N, const int32_t *acc, const float *as, const 
         }
 }
 
-/* W4A8 epilogue (no reference counterpart; BASELINE W4A8 configuration):
+/* W4A8 epilogue (no reference counterpart; the W4A8 linear with group-128 fp16 scales):
  * per-group int32 partials p[g][m][n], fp16 group scales gs[n][G];
  *   y = 0; for g in order: y = fma((float)p_g, gs[n][g], y)
  *   out = fp16(y * as[m] (+ bias[n])) */
