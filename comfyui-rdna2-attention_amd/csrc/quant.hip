@@ -23,12 +23,14 @@ struct ModArgs {
 #define QT 256  // threads per row
 
 // int8_gemm.hip:106-109
+// s - 2 x as one FMA: 2 x is exact, so fma(-2, x, s) rounds s - 2 x once, exactly as the separate product and
+// difference do.
 __device__ __forceinline__ void h4(float& a, float& b, float& c, float& d) {
     const float s = a + b + c + d, a0 = a, b0 = b;
-    a = s - 2.f * d;
-    b = s - 2.f * c;
-    c = s - 2.f * b0;
-    d = s - 2.f * a0;
+    a = __builtin_fmaf(-2.f, d, s);
+    b = __builtin_fmaf(-2.f, c, s);
+    c = __builtin_fmaf(-2.f, b0, s);
+    d = __builtin_fmaf(-2.f, a0, s);
 }
 __device__ __forceinline__ void h16(float (&v)[16]) {
 #pragma unroll
