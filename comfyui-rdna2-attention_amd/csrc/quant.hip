@@ -74,8 +74,12 @@ __device__ __forceinline__ bool silu_sure_tiny(float q) {
     const float ulp = __uint_as_float(__float_as_uint(r) & 0x7f800000u) * (1.f / 8388608.f);
     return r < 1024.f && fabsf(f - 0.5f) > SILU_T * ulp;
 }
-// int8_gemm.hip:135-137
-__device__ __forceinline__ float sigmoid_gate(float x, float gate) { return r16(x * r16(1.f / (1.f + rda_expf(-gate)))); }
+// int8_gemm.hip:135-137: r16(x r16(sigmoid(gate))), sigmoid(g) = 1 / (1 + rda_expf(-g)) in fp32. The kernel takes
+// sigmoid from the same kind of fast path as silu (hardware exp2 and reciprocal) where the result is sure to round
+// to the same fp16 value (silu_sure, silu_sure_tiny), and this exact formula elsewhere; the gate tests run every
+// finite fp16 gate through the kernel.
+__device__ __forceinline__ float sigmoid_exact(float g) { return 1.f / (1.f + rda_expf(-g)); }
+__device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
 // int8_gemm.hip:140-143
 __device__ __forceinline__ float modulate(float x, float rstd, float w, float s, float t) {
     return r16(r16(r16(x * rstd * (w + 1.f)) * s) + t);
@@ -187,11 +191,25 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
                 } else if (ACT == GATE) {
                     const half_t* u = U + (size_t)row * K;
                     const h8 ulo = *(const h8*)(u + e0), uhi = *(const h8*)(u + e0 + 8);
+                    float sg[16];
+                    bool unsure[16];
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        v[i] = sigmoid_gate((float)lo[i], (float)ulo[i]);
-                        v[8 + i] = sigmoid_gate((float)hi[i], (float)uhi[i]);
+                    for (int i = 0; i < 16; i++) {
+                        sg[i] = sigmoid_fast((float)(i < 8 ? ulo[i] : uhi[i - 8]));
+                        unsure[i] = !silu_sure(sg[i]);
                     }
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        if (__any(unsure[i])) {
+                            unsure[i] = unsure[i] && !silu_sure_tiny(sg[i]);
+                            if (__any(unsure[i])) {
+                                const float exact = sigmoid_exact((float)(i < 8 ? ulo[i] : uhi[i - 8]));
+                                if (unsure[i]) sg[i] = exact;
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; i++) v[i] = r16((float)(i < 8 ? lo[i] : hi[i - 8]) * r16(sg[i]));
                 } else if (ACT == MOD) {
                     const h8 slo = *(const h8*)(ms + e0), shi = *(const h8*)(ms + e0 + 8);
                     const h8 tlo = *(const h8*)(mt + e0), thi = *(const h8*)(mt + e0 + 8);

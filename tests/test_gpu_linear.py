@@ -74,6 +74,23 @@ def test_swiglu_every_fp16_gate(dev):
     assert_same(q_of(packed, M, K), q_ref)
 
 
+def test_gate_every_fp16_gate(dev):
+    """Every finite fp16 gate value through the sigmoid-gate kernel (whose sigmoid takes a fast path away from fp16
+    rounding midpoints): row r has x = 16 and gate g_r at element 0, x = 0 elsewhere. The rotated row is then
+    +-r16(16 r16(sigmoid(g_r))) / 16 in every element, exactly, so the row scale fixes r16(sigmoid(g_r))."""
+    g = np.arange(65536, dtype=np.uint16).view(np.float16)
+    g = g[np.isfinite(g)]
+    M, K = len(g), 256
+    x = np.zeros((M, K), np.float16)
+    x[:, 0] = 16
+    gate = np.zeros((M, K), np.float16)
+    gate[:, 0] = g
+    packed, scale = int8_gemm.quantize(kern().gate_rot_quant_pack_a, torch.from_numpy(x).to(dev), K, up=torch.from_numpy(gate).to(dev), group=256)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x, act=oracle.ACT_GATE, group=256, u=gate)
+    assert_same(scale.cpu().numpy(), s_ref)
+    assert_same(q_of(packed, M, K), q_ref)
+
+
 @pytest.mark.parametrize("B,L,K", [(1, 77, 3072), (2, 40, 1024)])
 def test_mod_rot_quant_bit_exact(dev, B, L, K):
     print(f"mod_rot_quant B={B} L={L} K={K}", flush=True)
