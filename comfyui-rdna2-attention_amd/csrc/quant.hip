@@ -20,7 +20,7 @@ struct ModArgs {
     float eps;
 };
 
-#define QT 256  // threads per row
+#define QT 256  // threads per row of the reference's kernels (rms_norm's summation order follows it)
 
 // int8_gemm.hip:106-109
 // s - 2 x as one FMA: 2 x is exact, so fma(-2, x, s) rounds s - 2 x once, exactly as the separate product and
@@ -95,9 +95,11 @@ __device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
     return (u32)(a & 255) | ((u32)(b & 255) << 8) | ((u32)(c & 255) << 16) | ((u32)(d & 255) << 24);
 }
 
-// GROUP 256 or 128 rotates; GROUP 0 is quant_pack_a (no rotation, int8_gemm.hip:93-103).
-template <int ACT, bool I4, int GROUP>
-__global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
+// GROUP 256 or 128 rotates; GROUP 0 is quant_pack_a (no rotation, int8_gemm.hip:93-103). NW waves per row: the
+// launcher sizes it to the row (K / 1024 waves, so that K = 3072 keeps every lane busy in both passes: the kernel
+// is vector-ALU bound); MOD keeps 4 (QT threads), whose sum of squares follows the reference's thread order.
+template <int ACT, bool I4, int GROUP, int NW>
+__global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
                                                        int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ float red[8];
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
     float mx = 0.f;
 
     if constexpr (GROUP == 0) {
-        for (int i = t; i < K / 8; i += QT) {
+        for (int i = t; i < K / 8; i += NW * 64) {
             const h8 v = ((const h8*)x)[i];
             ((h8*)rotated)[i] = v;
 #pragma unroll
@@ -131,6 +133,7 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
             }
 #pragma unroll
             for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+            static_assert(ACT != MOD || NW * 64 == QT, "the MOD sum of squares needs the reference's 256 threads");
             if ((t & 31) == 0) red[t >> 5] = sum;
             __syncthreads();
             float total = 0.f;
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
         const half_t* mt = ACT == MOD ? mod.t + mrow : nullptr;
         const float norm = GROUP == 256 ? 0.0625f : 0.0883883461356163025f;
 
-        for (int g0 = wave * GPW; g0 < groups; g0 += 4 * GPW) {
+        for (int g0 = wave * GPW; g0 < groups; g0 += NW * GPW) {
             const int g = g0 + gl;
             const bool active = g < groups;
             float v[16];
@@ -278,13 +281,15 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
     __syncthreads();
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
     const float scale = I4 ? fmaxf(mx, 1e-10f) / 7.f : fmaxf(mx / 127.f, 1e-30f);
     if (t == 0) as[row] = scale;
 
     const float rcp = 1.f / scale;
     int8_t* out = Aq + (size_t)row * K;
-    for (int ch = t; ch < K / 16; ch += QT) {
+    for (int ch = t; ch < K / 16; ch += NW * 64) {
         const h8 lo = ((const h8*)rotated)[ch * 2], hi = ((const h8*)rotated)[ch * 2 + 1];
         int q[16];
 #pragma unroll
@@ -301,13 +306,28 @@ __global__ __launch_bounds__(QT) void rot_quant_kernel(const half_t* __restrict_
     }
 }
 
+template <int ACT, bool I4, int GROUP, int NW>
+static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
+    const size_t lds = (size_t)K * 2 + (GROUP ? NW * 64 * 17 * sizeof(float) : 0);
+    hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
+                       (const half_t*)u, (int8_t*)aq, as, K, mod);
+    return (int)hipGetLastError();
+}
+
 template <int ACT, bool I4, int GROUP>
 static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
     if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || K > 16384) return RDA_ERR_INVALID;
-    const size_t lds = (size_t)K * 2 + (GROUP ? 4 * 64 * 17 * sizeof(float) : 0);
-    hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP>), dim3(M), dim3(QT), lds, (hipStream_t)stream, (const half_t*)x, ldx,
-                       (const half_t*)u, (int8_t*)aq, as, K, mod);
-    return (int)hipGetLastError();
+    if constexpr (ACT == MOD || GROUP == 0) {
+        return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
+    } else {
+        // One wave per 1024 values, up to four: every lane has a chunk in both passes when K is a multiple of 1024.
+        switch (K >= 4096 ? 4 : K <= 1024 ? 1 : K / 1024) {
+        case 1: return launch_rot_quant_nw<ACT, I4, GROUP, 1>(x, ldx, u, aq, as, M, K, mod, stream);
+        case 2: return launch_rot_quant_nw<ACT, I4, GROUP, 2>(x, ldx, u, aq, as, M, K, mod, stream);
+        case 3: return launch_rot_quant_nw<ACT, I4, GROUP, 3>(x, ldx, u, aq, as, M, K, mod, stream);
+        default: return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
+        }
+    }
 }
 
 template <int ACT, bool I4>
