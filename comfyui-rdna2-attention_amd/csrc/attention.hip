@@ -418,12 +418,8 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, void* out
 template <bool I8>
 static int launch_attn(const AttnArgs& a, void* stream) {
     const size_t lds = Tile<I8>::LDS;
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void*)attn_kernel<I8>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return (int)e;
-        configured = true;
-    }
+    static std::atomic<size_t> configured[RDA_MAX_DEVICES];
+    if (const int e = ensure_dynamic_lds((const void*)attn_kernel<I8>, lds, configured)) return e;
     hipLaunchKernelGGL(attn_kernel<I8>, dim3(a.nblocks), dim3(AT), lds, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }

@@ -23,6 +23,26 @@ typedef u32 u4v __attribute__((ext_vector_type(4)));
 
 #define RDA_ERR_INVALID 1  // hipErrorInvalidValue
 
+#include <atomic>
+
+#define RDA_MAX_DEVICES 64
+// Raises kernel `fn`'s dynamic-LDS limit to at least `bytes` on the current device, once per device and size:
+// `done` is the caller's record for that kernel (bytes configured per device; atomics, so that threads launching
+// at the same time at most repeat the call). Returns a hipError_t.
+static inline int ensure_dynamic_lds(const void* fn, size_t bytes, std::atomic<size_t> (&done)[RDA_MAX_DEVICES]) {
+    int dev = 0;
+    const hipError_t g = hipGetDevice(&dev);
+    if (g != hipSuccess) return (int)g;
+    if (dev < 0 || dev >= RDA_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    if (done[dev].load(std::memory_order_relaxed) >= bytes) return 0;
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return (int)e;
+    size_t prev = done[dev].load(std::memory_order_relaxed);
+    while (prev < bytes && !done[dev].compare_exchange_weak(prev, bytes, std::memory_order_relaxed)) {
+    }
+    return 0;
+}
+
 // fp32 -> fp16 (RNE) of a value that has been rounded to fp32 first. Without the register barrier the compiler
 // folds a preceding fp32 multiply or FMA into v_fma_mixlo_f16, which rounds the exact product once, straight to
 // fp16; every rounding point in these kernels is "round to fp32, then to fp16", as the arithmetic is written.

@@ -624,12 +624,8 @@ static int launch_gemm8(const void* a, const void* w, const float* as, const flo
     if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
     if (lds > 160 * 1024 / MINB - (size_t)(BN * 4 + SC_BIAS(BN) + BM * 4)) return -1;
     auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB>;
-    static int configured = 0;
-    if ((size_t)configured < lds) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return (int)e;
-        configured = (int)lds;
-    }
+    static std::atomic<size_t> configured[RDA_MAX_DEVICES];
+    if (const int e = ensure_dynamic_lds((const void*)kern, lds, configured)) return e;
     hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
                        (const half_t*)gs, (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
     return (int)hipGetLastError();
@@ -687,12 +683,8 @@ static int launch_gemm(const void* a, const void* w, const float* as, const floa
                        int group, const void* R, const void* G, int L, void* stream) {
     const size_t lds = (size_t)2 * (BM + BN) * PITCH;
     auto kern = gemm_kernel<BM, BN, WM, WN, W4, EPI>;
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return (int)e;
-        configured = true;
-    }
+    static std::atomic<size_t> configured[RDA_MAX_DEVICES];
+    if (const int e = ensure_dynamic_lds((const void*)kern, lds, configured)) return e;
     hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
                        (const half_t*)gs, (const half_t*)bias, c, M, N, K, group, (const half_t*)R, (const half_t*)G, L);
     return (int)hipGetLastError();
