@@ -383,33 +383,35 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 }
 
 // int8 GEMM with direct global->LDS copies, for int8 or packed int4 weights (PER_CHANNEL, GROUP_SCALED and
-// RAW_ACC epilogues). A workgroup of four wave64s computes a BM x BN tile, each wave a BM/2 x BN/2 quarter
-// of 32x32 blocks (accumulators in AGPRs; the products compute W A^T, so each lane ends up owning row
-// segments of C). K advances in slices of KB8 values through NS LDS stages: the copies of slice k + NS - 1
-// go out while slice k is multiplied. A stage holds the slice's BM A rows (KB8 bytes each), then its BN W
-// rows (KB8 bytes, or KB8 / 2 packed int4 bytes), with 16-byte chunk c of row r at c ^ ((r / RPL) % CPR)
-// (RPL rows per 256-byte bank line, CPR chunks per row): the fragment reads of 16 consecutive rows then hit
-// 16 distinct bank groups, and one 1 KiB copy instruction (lane i -> bytes 16 i) fills whole rows. int4
-// fragments are read as 8 bytes and widened to 16 int8 in registers with each nibble in the high half of its
-// byte, i.e. as 16 times its signed value (two ANDs and a shift, then v_perm interleaves the even-k low
+// RAW_ACC epilogues). A workgroup of four wave64s computes a BM x BN tile, the waves WGM x (4 / WGM) over
+// it (each a BM/2 x BN/2 quarter, or with WGM = 1 all BM rows and BN/4 columns) in 32x32 blocks (the
+// products compute W A^T, so each lane ends up owning row segments of C). K advances in slices of KB8
+// values through NS LDS stages: the copies of slice k + NS - 1 go out while slice k is multiplied. A stage
+// holds the slice's BM A rows (KB8 bytes each), then its BN W rows (KB8 bytes, or KB8 / 2 packed int4
+// bytes), with 16-byte chunk c of row r at c ^ ((r / RPL) % CPR) (RPL rows per 256-byte bank line, CPR
+// chunks per row): the fragment reads of 16 consecutive rows then hit 16 distinct bank groups, and one
+// 1 KiB copy instruction (lane i -> bytes 16 i) fills whole rows. int4 fragments are read as 8 bytes, first
+// in each k step, and widened after the step's last product to 16 int8 with each nibble in the high half of
+// its byte, i.e. as 16 times its signed value (two ANDs and a shift, then v_perm interleaves the even-k low
 // nibbles with the odd-k high nibbles); the accumulators then hold exactly 16 times the products, which the
 // kernel undoes after the K loop (an arithmetic shift of the int32 sums, a factor 1/16 on the fp32 group
 // sums: both exact). The host keeps K <= 65536 on this path so that 16 times the sums fits in 32 bits.
 //
 // GROUP_SCALED (group == KB8 == 128): the first product of each slice starts from zero and after the slice
 // the int32 partials are folded into fp32 sums, y = fma((float)p, gs[n, slice], y), in group order; the
-// block's group scales are staged in LDS as [group][column] at the start.
+// block's group scales are staged in LDS as [group][column] at the start, and each lane reads its slice's
+// scales at the slice's first product.
 //
-// One wave per SIMD, so nothing else hides the issue time of copies and LDS reads: every copy and
-// fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
+// One wave per SIMD (two with MINB = 2), so little else hides the issue time of copies and LDS reads: every
+// copy and fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM>
 __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
                                                       const float* __restrict__ ws, const half_t* __restrict__ gs, const half_t* __restrict__ bias,
                                                       void* __restrict__ Cout, int M, int N, int K, const half_t* __restrict__ R,
                                                       const half_t* __restrict__ G, int L) {
-    constexpr int TM = BM / 2, TN = BN / 2, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
+    constexpr int WGN = 4 / WGM, TM = BM / WGM, TN = BN / WGN, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
     constexpr bool GRP = EPI == GROUP_SCALED;
     constexpr int KS = KB8 / 32;                                      // 32-wide k steps per slice
     constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // A rows: chunks per row, rows per copy, rows per bank line
@@ -417,11 +419,11 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     constexpr int CPRB = WB / 16, RPIB = 1024 / WB, RPLB = 256 / WB;
     constexpr int STAGE = BM * KB8 + BN * WB;
     constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPIB), NI = AI + BI;  // copy instructions per wave per slice
-    static_assert((BM == 256 || BM == 128) && BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
+    static_assert((BM == 256 || BM == 128) && (WGM == 1 || WGM == 2) && BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
     static_assert(!GRP || KB8 == 128, "one group per slice");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave >> 1, wn = wave & 1;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), wm = wave / WGN, wn = wave % WGN;
 
     // Tile order: block ids go round-robin to the 8 XCDs. When the grid allows it, XCD x gets the tiles of
     // one (gy / 2) x (gx / 4) sub-grid, so each A row panel is read by 4 XCDs' L2s and each W panel by 2
@@ -492,13 +494,18 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     };
 
     // Fragment f (< FI: A block f, else W block f - FI) of k step kk: row base + lq, k values 32 kk + 16 g ..
-    // + 15, i.e. chunk 2 kk + g of an A row, the half g of chunk kk of a packed int4 W row.
+    // + 15, i.e. chunk 2 kk + g of an A row, the half g of chunk kk of a packed int4 W row. A packed int4
+    // fragment is read as its 8 bytes (wraw) and widened later (widen), so that products, not the widening,
+    // wait for the read.
     const int fx = (lq / RPL) % CPR, fxb = (lq / RPLB) % CPRB;
     auto frag = [&](const char* st, int kk, int f) -> i4v {
         if (f < FI) return *(const i4v*)(st + (wm * TM + f * 32 + lq) * KB8 + (((2 * kk + g) ^ fx) << 4));
-        const char* wr = st + BM * KB8 + (wn * TN + (f - FI) * 32 + lq) * WB;
-        if (!W4) return *(const i4v*)(wr + (((2 * kk + g) ^ fxb) << 4));
-        const u2v p = *(const u2v*)(wr + ((kk ^ fxb) << 4) + 8 * g);
+        return *(const i4v*)(st + BM * KB8 + (wn * TN + (f - FI) * 32 + lq) * WB + (((2 * kk + g) ^ fxb) << 4));
+    };
+    auto wraw = [&](const char* st, int kk, int j) -> u2v {
+        return *(const u2v*)(st + BM * KB8 + (wn * TN + j * 32 + lq) * WB + ((kk ^ fxb) << 4) + 8 * g);
+    };
+    auto widen = [](u2v p) -> i4v {
         u4v o;
 #pragma unroll
         for (int d = 0; d < 2; d++) {
@@ -519,7 +526,8 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
         for (int i = 0; i < FI; i++)
 #pragma unroll
             for (int j = 0; j < FJ; j++) yacc[GRP ? i : 0][GRP ? j : 0] = (f16v){};
-    i4v fr[2][NR];  // fragments of the current and the next k step
+    i4v fr[2][NR];            // fragments of the current and the next k step
+    u2v fw[W4 ? FJ : 1];      // packed int4 W fragments of the next k step, before widening
 
     const int KT = K / KB8;
 #pragma unroll
@@ -532,7 +540,7 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     else wait_copies();
     __syncthreads();
 #pragma unroll
-    for (int f = 0; f < NR; f++) fr[0][f] = frag(stage(0), 0, f);
+    for (int f = 0; f < NR; f++) fr[0][f] = W4 && f >= FI ? widen(wraw(stage(0), 0, f - FI)) : frag(stage(0), 0, f);
 
     // Copies of a slice are spread over its first CKS k steps: k step ks issues copies [CB(ks), CB(ks + 1)).
     // With two stages the copies of slice k + 1 go out during slice k, so all of them must precede the
@@ -542,12 +550,23 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     // Copies that may still be in flight at that barrier once slice k + 1 has landed: the NS - 3 slices
     // after it, and the part of slice k + NS - 1 issued before the barrier.
     constexpr int LEFT = NS == 2 ? 0 : (NS - 3) * NI + CB(KS - 1);
+    // Order of the next step's fragment reads over the products: int4 W fragments first, so that they have
+    // landed when they are widened after the step's last product.
+    constexpr auto RD = [](int f) { return W4 ? (f >= FI ? f - FI : f + FJ) : f; };
+    // GROUP_SCALED: each lane's group scales of a slice, read at its first product, used by its fold. The
+    // per-lane offset is held opaque so the slice's reads are one base plus immediate offsets.
+    u32 goff = 0;
+    if constexpr (GRP) {
+        goff = (u32)(GS_OFF + (wn * TN + 4 * g) * 2);
+        asm volatile("" : "+v"(goff));
+    }
     // One slice. AHEAD: slice kt + NS - 1 exists and is copied now (into the stage of slice kt - 1, whose
     // reads ended before the last barrier); MORE: slice kt + 1 exists.
     auto slice = [&](int kt, auto ahead, auto more) {
         constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
         const char* st = stage(kt);
         const char* sn = stage(kt + 1);
+        h4v gv[GRP ? FJ : 1][4];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             if (ks == KS - 1) {
@@ -566,10 +585,22 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
 #pragma unroll
                     for (int c = 0; c < nc; c++)
                         if (c * NF / nc == p) copy(kt + NS - 1, CB(ks) + c);
-                if (!last || MORE)
+                if (GRP && ks == 0 && p == 0)
 #pragma unroll
-                    for (int f = 0; f < NR; f++)
-                        if ((f * NF + NF / 2) / NR == p) fr[nxt][f] = last ? frag(sn, 0, f) : frag(st, ks + 1, f);
+                    for (int j = 0; j < FJ; j++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++) gv[GRP ? j : 0][q] = *(const h4v*)(smem + goff + kt * BN * 2 + (j * 32 + 8 * q) * 2);
+                if (!last || MORE) {
+#pragma unroll
+                    for (int f = 0; f < NR; f++) {
+                        if ((RD(f) * NF + NF / 2) / NR != p) continue;
+                        if (W4 && f >= FI) fw[W4 ? f - FI : 0] = last ? wraw(sn, 0, f - FI) : wraw(st, ks + 1, f - FI);
+                        else fr[nxt][f] = last ? frag(sn, 0, f) : frag(st, ks + 1, f);
+                    }
+                    if (W4 && p == NF - 1)
+#pragma unroll
+                        for (int j = 0; j < FJ; j++) fr[nxt][FI + j] = widen(fw[W4 ? j : 0]);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -579,12 +610,12 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
             for (int j = 0; j < FJ; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const h4v gv = *(const h4v*)(gsl + kt * BN + wn * TN + j * 32 + 8 * q + 4 * g);
 #pragma unroll
                     for (int i = 0; i < FI; i++)
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e] = __builtin_fmaf((float)acc[i][j][4 * q + e], (float)gv[e], yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e]);
+                            yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e] =
+                                __builtin_fmaf((float)acc[i][j][4 * q + e], (float)gv[GRP ? j : 0][q][e], yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e]);
                 }
         }
     };
@@ -615,7 +646,7 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     }
 }
 
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1, int WGM = 2>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                         const void* R, const void* G, int L, void* stream) {
     const size_t stage = (size_t)BM * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
@@ -623,7 +654,7 @@ static int launch_gemm8(const void* a, const void* w, const float* as, const flo
     size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
     if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
     if (lds > 160 * 1024 / MINB - (size_t)(BN * 4 + SC_BIAS(BN) + BM * 4)) return -1;
-    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB>;
+    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB, WGM>;
     static std::atomic<size_t> configured[RDA_MAX_DEVICES];
     if (const int e = ensure_dynamic_lds((const void*)kern, lds, configured)) return e;
     hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
@@ -658,10 +689,11 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
     auto aligned = [](const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; };
     if (!aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
     if constexpr (EPI == GROUP_SCALED) {
-        // One group per 128-wide slice. 128 x 128 blocks (64 x 64 per wave) leave room for two blocks per CU, so
-        // one block's group folds (vector ALU) overlap the other's products.
+        // One group per 128-wide slice. 128 x 128 blocks leave room for two blocks per CU, so one block's group
+        // folds (vector ALU) overlap the other's products. Each wave takes all 128 rows and 32 columns: one int4
+        // fragment to widen per k step instead of two (as 64 x 64), for two more A fragment reads from LDS.
         if (group != 128 || K % 128 != 0 || N % 128 != 0) return -1;
-        return launch_gemm8<128, 128, 128, 3, W4, EPI, 2>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        return launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
     } else {
         // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
         const bool wide = K % 128 == 0;
