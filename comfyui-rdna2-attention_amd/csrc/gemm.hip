@@ -386,7 +386,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 // RAW_ACC epilogues). A workgroup of four wave64s computes a BM x BN tile, the waves WGM x (4 / WGM) over
 // it (each a BM/2 x BN/2 quarter, or with WGM = 1 all BM rows and BN/4 columns) in 32x32 blocks (the
 // products compute W A^T, so each lane ends up owning row segments of C). K advances in slices of KB8
-// values through NS LDS stages: the copies of slice k + NS - 1 go out while slice k is multiplied. A stage
+// values through NS LDS stages: the copies of slice k + NS go out during the last k step of slice k. A stage
 // holds the slice's BM A rows (KB8 bytes each), then its BN W rows (KB8 bytes, or KB8 / 2 packed int4
 // bytes), with 16-byte chunk c of row r at c ^ ((r / RPL) % CPR) (RPL rows per 256-byte bank line, CPR
 // chunks per row): the fragment reads of 16 consecutive rows then hit 16 distinct bank groups, and one
@@ -403,7 +403,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 // scales at the slice's first product.
 //
 // One wave per SIMD (two with MINB = 2), so little else hides the issue time of copies and LDS reads: every
-// copy and fragment read is issued in the shadow of a product, spread evenly over each 32-wide k step
+// copy and fragment read is issued in the shadow of a product, spread evenly over its 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
 template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM>
@@ -529,27 +529,26 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     i4v fr[2][NR];            // fragments of the current and the next k step
     u2v fw[W4 ? FJ : 1];      // packed int4 W fragments of the next k step, before widening
 
+    // Copy schedule: a slice's stage is free once the barrier before the slice's last k step has passed
+    // (every wave has then read its fragments of the slice), so the copies of slice k + NS go out during
+    // that last k step, into that stage, NS - 1 slices of products before they are needed. (Spreading the
+    // copies of slice k + NS - 1 over slice k instead left the last of them one k step to land.)
     const int KT = K / KB8;
 #pragma unroll
-    for (int kt = 0; kt < NS - 1; kt++)
+    for (int kt = 0; kt < NS; kt++)
         if (kt < KT)
 #pragma unroll
             for (int c = 0; c < NI; c++) copy(kt, c);
-    // Slice 0 must have landed; up to NS - 2 later slices may still be in flight.
-    if (KT >= NS - 1) wait_copies_but<(NS - 2) * NI>();
+    // Slice 0 must have landed; up to NS - 1 later slices may still be in flight.
+    if (KT >= NS) wait_copies_but<(NS - 1) * NI>();
     else wait_copies();
     __syncthreads();
 #pragma unroll
     for (int f = 0; f < NR; f++) fr[0][f] = W4 && f >= FI ? widen(wraw(stage(0), 0, f - FI)) : frag(stage(0), 0, f);
 
-    // Copies of a slice are spread over its first CKS k steps: k step ks issues copies [CB(ks), CB(ks + 1)).
-    // With two stages the copies of slice k + 1 go out during slice k, so all of them must precede the
-    // barrier that publishes it (before the last k step); with more stages they may follow it.
-    constexpr int CKS = NS == 2 ? KS - 1 : KS;
-    constexpr auto CB = [](int ks) { return (ks < CKS ? ks : CKS) * NI / CKS; };
-    // Copies that may still be in flight at that barrier once slice k + 1 has landed: the NS - 3 slices
-    // after it, and the part of slice k + NS - 1 issued before the barrier.
-    constexpr int LEFT = NS == 2 ? 0 : (NS - 3) * NI + CB(KS - 1);
+    // Copies that may still be in flight at the barrier of slice k once slice k + 1 has landed: the NS - 2
+    // slices after it.
+    constexpr int LEFT = (NS - 2) * NI;
     // Order of the next step's fragment reads over the products: int4 W fragments first, so that they have
     // landed when they are widened after the step's last product.
     constexpr auto RD = [](int f) { return W4 ? (f >= FI ? f - FI : f + FJ) : f; };
@@ -560,8 +559,8 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
         goff = (u32)(GS_OFF + (wn * TN + 4 * g) * 2);
         asm volatile("" : "+v"(goff));
     }
-    // One slice. AHEAD: slice kt + NS - 1 exists and is copied now (into the stage of slice kt - 1, whose
-    // reads ended before the last barrier); MORE: slice kt + 1 exists.
+    // One slice. AHEAD: slice kt + NS exists and is copied during this slice's last k step (then slices
+    // kt + 2 .. kt + NS - 1 exist too); MORE: slice kt + 1 exists.
     auto slice = [&](int kt, auto ahead, auto more) {
         constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
         const char* st = stage(kt);
@@ -576,15 +575,14 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
             }
             const int cur = ks & 1, nxt = cur ^ 1;
             const bool last = ks == KS - 1;
-            const int nc = CB(ks + 1) - CB(ks);
 #pragma unroll
             for (int p = 0; p < NF; p++) {
                 const i16v c0 = GRP && ks == 0 ? (i16v){} : acc[p / FJ][p % FJ];
                 acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[cur][FI + p % FJ], fr[cur][p / FJ], c0, 0, 0, 0);
-                if (AHEAD)
+                if (AHEAD && ks == KS - 1)
 #pragma unroll
-                    for (int c = 0; c < nc; c++)
-                        if (c * NF / nc == p) copy(kt + NS - 1, CB(ks) + c);
+                    for (int c = 0; c < NI; c++)
+                        if (c * NF / NI == p) copy(kt + NS, c);
                 if (GRP && ks == 0 && p == 0)
 #pragma unroll
                     for (int j = 0; j < FJ; j++)
@@ -622,7 +620,7 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
     int kt = 0;
-    for (; kt + NS - 1 < KT; kt++) slice(kt, yes{}, yes{});
+    for (; kt + NS < KT; kt++) slice(kt, yes{}, yes{});
     for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{});
     slice(kt, no{}, no{});
     if constexpr (W4) {  // the int4 operands were 16 times their values: undo it (exactly)
@@ -736,9 +734,9 @@ static int dispatch(const void* a, const void* w, const float* as, const float* 
         if (N % 256 == 0) return launch_gemm<128, 256, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
         return launch_gemm<256, 64, 4, 1, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
     } else {
-    if (N % 256 == 0) return launch_gemm<256, 256, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
-    if (N % 128 == 0) return launch_gemm<256, 128, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
-    return launch_gemm<256, 64, 4, 1, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
+        if (N % 256 == 0) return launch_gemm<256, 256, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
+        if (N % 128 == 0) return launch_gemm<256, 128, 2, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
+        return launch_gemm<256, 64, 4, 1, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
     }
 }
 

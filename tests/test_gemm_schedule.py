@@ -1,0 +1,113 @@
+"""A CPU model of the copy / wait / barrier schedule of gemm8_kernel (csrc/gemm.hip), checked for races.
+
+The kernel streams K in KT slices through NS LDS stages (slice s lives in stage s % NS). Each wave issues NI
+asynchronous global->LDS copies per slice; `wait_copies_but<T>` retires its oldest copies until at most T are
+outstanding (vmcnt counts loads in issue order); `__syncthreads` separates barrier epochs. The schedule:
+
+  prologue: copy slices 0 .. NS-1 (those that exist); wait until (NS-1) NI remain if KT >= NS, else all; barrier;
+            read the fragments of (slice 0, k step 0).
+  slice kt (AHEAD = kt + NS < KT, MORE = kt + 1 < KT), k steps ks = 0 .. KS-1:
+            at ks = KS-1 first: wait until (NS-2) NI remain if AHEAD, else all; barrier;
+            products of (kt, ks); if AHEAD and ks = KS-1: copy slice kt + NS (into stage kt % NS);
+            read the fragments of the next step: (kt, ks+1) if ks < KS-1, else (kt+1, 0) if MORE.
+
+All waves run the same program, and two events of different waves are ordered only when a barrier separates
+them. The model checks, for every wave pair at once:
+  * a fragment read of slice s happens in a later epoch than the wait that retired all of s's copies (so after
+    the barrier every wave's copies of s have landed), and the stage then holds s;
+  * a copy into a stage is issued in a later epoch than every read of the slice that stage held before;
+  * nothing reads or copies a slice that does not exist, and every slice is read.
+A schedule mistake (copying one slice later than the stages allow, a wait threshold one slice too loose, the
+barrier before the copies of the last k step dropped) fails one of these; test_model_catches_mistakes plants
+each of them.
+"""
+import pytest
+
+
+def run_schedule(NS, KS, KT, NI=3, left=None, prologue_keep=None, copy_at=None, barrier_last=True):
+    left = (NS - 2) * NI if left is None else left
+    prologue_keep = ((NS - 1) * NI if KT >= NS else 0) if prologue_keep is None else prologue_keep
+    copy_at = KS - 1 if copy_at is None else copy_at
+    epoch = 0
+    inflight = []  # slices of outstanding copies, in issue order
+    landed_epoch = {}  # slice -> epoch of the wait that retired its last copy
+    issued = {}  # slice -> number of copies issued
+    holder = {}  # stage -> slice last copied into it
+    last_read = {}  # slice -> epoch of its last fragment read
+    errors = []
+
+    def copy(s):
+        if not 0 <= s < KT:
+            errors.append(f"copy of missing slice {s}")
+            return
+        st = s % NS
+        prev = holder.get(st)
+        if prev is not None and last_read.get(prev, -1) >= epoch:
+            errors.append(f"slice {s} copied into stage {st} in epoch {epoch} while slice {prev} is read there")
+        holder[st] = s
+        for _ in range(NI):
+            inflight.append(s)
+        issued[s] = issued.get(s, 0) + NI
+
+    def wait(keep):
+        while len(inflight) > keep:
+            s = inflight.pop(0)
+            if s not in inflight:
+                landed_epoch[s] = epoch
+
+    def barrier():
+        nonlocal epoch
+        epoch += 1
+
+    def read(s):
+        if not 0 <= s < KT:
+            errors.append(f"read of missing slice {s}")
+            return
+        if landed_epoch.get(s, epoch) >= epoch or issued.get(s, 0) != NI:
+            errors.append(f"slice {s} read in epoch {epoch} before its copies landed")
+        if holder.get(s % NS) != s:
+            errors.append(f"slice {s} read from stage {s % NS}, which holds slice {holder.get(s % NS)}")
+        last_read[s] = epoch
+
+    for s in range(min(NS, KT)):
+        copy(s)
+    wait(prologue_keep)
+    barrier()
+    read(0)
+    for kt in range(KT):
+        ahead, more = kt + NS < KT, kt + 1 < KT
+        for ks in range(KS):
+            if ks == KS - 1:
+                wait(left if ahead else 0)
+                if barrier_last:
+                    barrier()
+            if ahead and ks == copy_at:
+                copy(kt + NS)
+            if ks < KS - 1:
+                read(kt)
+            elif more:
+                read(kt + 1)
+    if set(last_read) != set(range(KT)):
+        errors.append("not every slice was read")
+    return errors
+
+
+# (NS, KS): the kernel's configurations -- 128-byte slices (4 k steps) in 2 or 3 stages, 64-byte slices
+# (2 k steps) in 4 stages -- plus neighbours.
+@pytest.mark.parametrize("NS,KS", [(2, 4), (3, 4), (4, 2), (2, 2), (3, 2), (4, 4), (5, 2)])
+@pytest.mark.parametrize("KT", list(range(1, 13)) + [24, 64])
+def test_schedule_is_race_free(NS, KS, KT):
+    assert run_schedule(NS, KS, KT) == []
+
+
+@pytest.mark.parametrize("NS,KS", [(2, 4), (3, 4), (4, 2)])
+def test_model_catches_mistakes(NS, KS):
+    KT, NI = 10, 3
+    # a wait that lets the next slice's copies stay in flight
+    assert run_schedule(NS, KS, KT, NI, left=(NS - 1) * NI)
+    # a prologue that does not wait for slice 0
+    assert run_schedule(NS, KS, KT, NI, prologue_keep=NS * NI)
+    # copies issued before the barrier of the last k step (the stage may still be read by another wave)
+    assert run_schedule(NS, KS, KT, NI, copy_at=KS - 2)
+    # the barrier before the last k step dropped
+    assert run_schedule(NS, KS, KT, NI, barrier_last=False)
