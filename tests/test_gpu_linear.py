@@ -136,7 +136,7 @@ def test_gemm_int32_accumulators_exact(dev, M, N, K):
     assert_same(acc.cpu().numpy(), oracle.gemm_acc(a, w.numpy()))
 
 
-@pytest.mark.parametrize("M,N,K", [(600, 256, 1024), (128, 64, 256), (1000, 384, 512)])
+@pytest.mark.parametrize("M,N,K", [(600, 256, 1024), (128, 64, 256), (1000, 384, 512), (300, 192, 1408)])
 def test_gemm_int4_weight_accumulators_exact(dev, M, N, K):
     print(f"gemm_acc int4 M={M} N={N} K={K}", flush=True)
     a = torch.randint(-128, 128, (M, K), generator=gen(1), dtype=torch.int8).numpy()
@@ -189,7 +189,8 @@ def test_swiglu_down_linear_bit_exact(dev):
     assert_same(bits(out), bits(ref))
 
 
-@pytest.mark.parametrize("M,N,K", [(520, 512, 1024), (300, 192, 512), (4096, 1024, 3072)])
+# K / 128 = 8, 4, 24 and 26 slices: whole and partial passes of the slice loop over the three stages
+@pytest.mark.parametrize("M,N,K", [(520, 512, 1024), (300, 192, 512), (4096, 1024, 3072), (200, 256, 3328)])
 def test_w4a8_bit_exact(dev, M, N, K):
     print(f"w4a8 M={M} N={N} K={K}", flush=True)
     x = activations(M, K, seed=7, outliers=0)
