@@ -54,6 +54,8 @@ def attention(q, k, v, out, scale, int8_qk=False):
             raise ValueError("attention expects (B, H, L, 128) fp16 GPU tensors with a contiguous last dimension")
     b, heads, q_len, _ = q.shape
     _, kv_heads, k_len, _ = k.shape
+    if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)
+        return
     strides = _lib.long_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
     p = _lib.ptr
     if int8_qk:

@@ -83,6 +83,8 @@ def run(quant, gemm, x, weight, weight_scale, bias, K, up=None, activations=None
     M = x.shape[0]
     N = weight.shape[0]
     out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)
+        return out
     packed_a, a_scale = quantize(quant, x, K, up, group) if activations is None else activations
     p = _lib.ptr
     if gemm is k.gemm_i4:
@@ -109,6 +111,8 @@ def linear_w4a8(x, qweight, group_scales, bias=None, rotate=True, group=ROT_GROU
     k = get_kernels()
     M, K = x.shape
     N = qweight.shape[0]
+    if M == 0 or N == 0:
+        return torch.empty((M, N), dtype=torch.float16, device=x.device)
     if activations is None:
         activations = quantize(k.rot_quant_pack_a if rotate else k.quant_pack_a, x, K, None, group)
     packed_a, a_scale = activations

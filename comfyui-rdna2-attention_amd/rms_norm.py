@@ -41,6 +41,8 @@ def rms_norm(x, weight, eps):
     B, H, L, D = rows.shape
     sb, sh, sl = rows.stride()[:3]
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)
+        return out
     entry = k.rms_norm_head if D <= HEAD_DIM else k.rms_norm_row
     p = _lib.ptr
     launch(entry, 0, 0, THREADS, [p(x), p(weight), p(out), B, H, L, D, sb, sh, sl, float(eps)])
@@ -51,6 +53,8 @@ def rms_norm_rope(x, heads, module, freqs):
     """x is (B, L, heads * 128) fp16 and freqs (B or 1, 1, L, 64, 2, 2) fp32. Returns (B, heads, L, 128) with QK-norm and rope applied."""
     B, L, _ = x.shape
     out = torch.empty((B, heads, L, HEAD_DIM), dtype=x.dtype, device=x.device)
+    if out.numel() == 0:
+        return out
     weight = _weight_fp32(module.scale, x.device)
     batch_stride = L * HEAD_DIM // 2 if freqs.shape[0] > 1 else 0
     p = _lib.ptr
