@@ -126,7 +126,9 @@ def packed_from(a_int8):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 3072, 3072), (1000, 192, 512), (513, 64, 64), (256, 256, 8192), (77, 128, 1024), (300, 320, 192),
-                                   (512, 3072, 6144)])  # the last: the shape of the reference's gemm_k6144 (int8_gemm.hip:414)
+                                   (512, 3072, 6144),  # the shape of the reference's gemm_k6144 (int8_gemm.hip:414)
+                                   # the reference's own GEMM check shapes (prototypes/bg.py:26, given there as M, K, N)
+                                   (4056, 8192, 2048), (4056, 2048, 8192), (4056, 2048, 2048), (3014, 16384, 3072)])
 def test_gemm_int32_accumulators_exact(dev, M, N, K):
     print(f"gemm_acc M={M} N={N} K={K}", flush=True)
     g = gen(M + N + K)
