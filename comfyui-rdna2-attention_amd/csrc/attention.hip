@@ -425,6 +425,10 @@ static int launch_attn(const AttnArgs& a, void* stream) {
 }
 
 // Row strides of K and V must keep a tile's 32 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
+// K and V reach LDS by 16-byte global->LDS copies: their base addresses and their (batch, head, row) strides must
+// keep every row 16-byte aligned.
+static bool dma_ready(const void* p, long sb, long sh, long sl) { return ((uintptr_t)p & 15) == 0 && sb % 8 == 0 && sh % 8 == 0 && sl % 8 == 0; }
+
 static bool attn_shapes_ok(int B, int H, int Hkv, int Lq, int Lk, const long* st) {
     const bool rows_ok = st[5] >= 0 && st[5] < (1L << 24) && st[8] >= 0 && st[8] < (1L << 24);
     return B > 0 && H > 0 && Hkv > 0 && H % Hkv == 0 && Lq > 0 && Lk > 0 && (long)B * H * ((Lq + QB - 1) / QB) < (1L << 31) && rows_ok;
@@ -440,6 +444,7 @@ size_t rda_attn_i8_workspace(int B, int Hkv, int Lk) {
 int rda_attn(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
              void* stream) {
     if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
+    if (!dma_ready(k, strides[3], strides[4], strides[5]) || !dma_ready(v, strides[6], strides[7], strides[8])) return RDA_ERR_INVALID;
     return launch_attn<false>(make_args(q, k, v, out, B, H, Hkv, Lq, Lk, strides, scale), stream);
 }
 
@@ -456,6 +461,7 @@ int rda_pack_k_i8(const void* k, void* workspace, int B, int Hkv, int Lk, long s
 int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
                 float scale, void* stream) {
     if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
+    if (((uintptr_t)workspace & 15) != 0 || !dma_ready(v, strides[6], strides[7], strides[8])) return RDA_ERR_INVALID;
     AttnArgs a = make_args(q, nullptr, v, out, B, H, Hkv, Lq, Lk, strides, scale);
     a.k8 = (const int8_t*)workspace;
     a.ks = (const float*)(a.k8 + (size_t)B * Hkv * a.Lk_pad * 128);

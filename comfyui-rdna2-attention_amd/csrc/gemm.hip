@@ -700,7 +700,8 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
     if (W4 && K > 65536) return -1;  // 16 x the int4 products, summed over K, must fit in int32
     // The row-segment epilogue reads ws as float4 and bias / R / G and writes C as 8-byte (int32: 16-byte) vectors.
     auto aligned = [](const void* p, uintptr_t al) { return ((uintptr_t)p & (al - 1)) == 0; };
-    if (!aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
+    // A and W reach LDS by 16-byte global->LDS copies (rows stay aligned: K % 64 == 0).
+    if (!aligned(a, 16) || !aligned(w, 16) || !aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
     if constexpr (EPI == GROUP_SCALED) {
         // One group per 128-wide slice. 128 x 128 blocks leave room for two blocks per CU, so one block's group
         // folds (vector ALU) overlap the other's products. Each wave takes all 128 rows and 32 columns: one int4

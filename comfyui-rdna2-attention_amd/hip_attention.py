@@ -43,6 +43,11 @@ def launch(func, grid_x, grid_y, block, args, shared=0):
 kernels = None
 
 
+def _dma_ready(t):
+    """K and V rows reach LDS by 16-byte copies: a 16-byte aligned start and (batch, head, row) strides of 8 values."""
+    return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3])
+
+
 def attention(q, k, v, out, scale, int8_qk=False):
     """q, k, v, out are (batch, heads, length, 128) fp16 tensors with a contiguous last dimension. k and v may have
     fewer heads than q, which then share them. out is written in place."""
@@ -56,6 +61,7 @@ def attention(q, k, v, out, scale, int8_qk=False):
     _, kv_heads, k_len, _ = k.shape
     if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)
         return
+    k, v = (t if _dma_ready(t) else t.clone(memory_format=torch.contiguous_format) for t in (k, v))
     strides = _lib.long_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
     p = _lib.ptr
     if int8_qk:

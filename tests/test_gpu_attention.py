@@ -112,3 +112,33 @@ def test_attention_full_size_sampled(dev):
             fn = oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64
             ref = fn(qs.numpy(), k[:, h:h + 1].numpy(), v[:, h:h + 1].numpy(), scale)
             close(o[:, h:h + 1, rows], ref)
+
+
+@pytest.mark.parametrize("int8_qk", [False, True])
+def test_attention_unaligned_kv_views(dev, int8_qk):
+    """K and V views that start 4 bytes into their storage (not 16-byte aligned, as the kernel's global->LDS copies
+    need): the wrapper copies them, and the result equals the one from aligned tensors."""
+    q, k, v = qkv(1, 2, 2, 100, 300, seed=21)
+    kb = torch.empty(k.numel() + 2, dtype=torch.float16, device=dev)
+    vb = torch.empty(v.numel() + 2, dtype=torch.float16, device=dev)
+    ku, vu = kb[2:].view(k.shape), vb[2:].view(v.shape)
+    ku.copy_(k.to(dev))
+    vu.copy_(v.to(dev))
+    assert ku.data_ptr() % 16 != 0 and vu.data_ptr() % 16 != 0
+    out_u = torch.empty(1, 2, 100, 128, dtype=torch.float16, device=dev)
+    out_a = torch.empty_like(out_u)
+    hip_attention.attention(q.to(dev), ku, vu, out_u, 128 ** -0.5, int8_qk)
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out_a, 128 ** -0.5, int8_qk)
+    assert torch.equal(out_u.view(torch.int16), out_a.view(torch.int16))
+
+
+def test_attention_abi_rejects_unaligned_kv(dev):
+    """The C entry point itself refuses K / V rows that are not 16-byte aligned (invalid-argument error)."""
+    q, k, v = (t.to(dev) for t in qkv(1, 1, 1, 32, 64, seed=22))
+    kb = torch.empty(k.numel() + 2, dtype=torch.float16, device=dev)
+    ku = kb[2:].view(k.shape)
+    out = torch.empty_like(q)
+    lib = _lib.load()
+    strides = _lib.long_array([*q.stride()[:3], *ku.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
+    p = _lib.ptr
+    assert lib.rda_attn(p(q), p(ku), p(v), p(out), 1, 1, 1, 32, 64, strides, 128 ** -0.5, _lib.stream()) == 1

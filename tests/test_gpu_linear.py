@@ -235,3 +235,19 @@ def test_rejects_unsupported_shapes(dev):
     x = activations(8, 100, seed=1)
     with pytest.raises(RuntimeError, match="HIP error 1"):
         int8_gemm.quantize(kern().rot_quant_pack_a, x.to(dev), 100)
+
+
+def test_w8a8_linear_unaligned_weight_view(dev):
+    """A weight view that starts 4 bytes into its storage (not 16-byte aligned, as the direct-copy kernel needs) is
+    served by the register-load GEMM, bit-exact all the same."""
+    M, N, K = 600, 256, 1024
+    x = activations(M, K, seed=31)
+    w = int8_weights(N, K, seed=32)
+    ws = channel_scales(N, seed=33)
+    buf = torch.empty(N * K + 4, dtype=torch.int8, device=dev)
+    wu = buf[4:].view(N, K)
+    wu.copy_(w.to(dev))
+    assert wu.data_ptr() % 16 != 0
+    out = int8_gemm.linear(x.to(dev), wu, ws.to(dev), None, rotate=True)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())))
