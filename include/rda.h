@@ -81,7 +81,9 @@ int rda_gemm_acc(const void* a_q, const void* w, int w_int4, void* acc, int M, i
 /* ------------------------------------------------------------------ attention ------------ */
 /* q, out (B, H, Lq, 128) fp16 and k, v (B, Hkv, Lk, 128) fp16 with a contiguous last dimension;
  * strides[12] = element strides (batch, head, row) of q, k, v, out. scale is the softmax scale
- * (the kernels use scale * log2 e). */
+ * (the kernels use scale * log2 e). k and v (and the int8-QK workspace) must start 16-byte aligned
+ * with strides that are multiples of 8 (their rows are copied to LDS 16 bytes at a time); other
+ * layouts are rejected with 1. */
 
 /* attn (+ pack_kv), hip_attention.py:61-66 (hip_attention.hip:30-54, 280-373). No workspace. */
 int rda_attn(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
