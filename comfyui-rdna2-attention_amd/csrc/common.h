@@ -165,6 +165,11 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // bookkeeping: the compiler cannot tell the LDS stage they fill from the stage being read and would
 // otherwise make every LDS read wait for the copies in flight. A kernel waits for its copies itself
 // (wait_copies, wait_copies_but) before the barrier that hands a stage over.
+// They set m0 (the copies' LDS base), a register the compiler reserves; clang warns that such a clobber may not
+// be honoured. Nothing else in these kernels uses m0 (tests/test_abi.py checks the generated code: every m0
+// reference is the s_mov_b32 of one of these copies), so the warning is silenced here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ u32 lds_addr(const char* p) { return (u32)(uintptr_t)(const lds_void_t*)p; }
 __device__ __forceinline__ void dma16(const void* base, u32 off, const char* lds) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds_addr(lds)) : "memory", "m0");
@@ -175,6 +180,7 @@ __device__ __forceinline__ void dma4(const void* base, u32 off, const char* lds)
 __device__ __forceinline__ void dma16_at(const void* src, const char* lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 __device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Waits until at most N of this wave's copies are outstanding (they complete in issue order).
 template <int N>

@@ -54,3 +54,29 @@ def test_no_cpu_fallback_without_gpu(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         _lib.load()
+
+
+def test_m0_is_only_set_by_the_copies(tmp_path):
+    """The global->LDS copy helpers (csrc/common.h) set m0 from asm with the compiler's warning about clobbering a
+    reserved register silenced: that is sound only while no other code in the kernels uses m0. Every m0 reference in
+    the generated gfx950 code must be the copies' own `s_mov_b32 m0, s<n>`."""
+    import shutil
+    import importlib.util
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc is not installed")
+    spec = importlib.util.spec_from_file_location("rda_build", os.path.join(ROOT, "comfyui-rdna2-attention_amd", "build.py"))
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    setter = re.compile(r"^s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)$")
+    for src in build.sources():
+        asm = tmp_path / (os.path.basename(src) + ".s")
+        flags = [f for f in build.HIPFLAGS if f != "-fPIC"] + build.FILE_FLAGS.get(os.path.basename(src), [])
+        subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", src, "-o", str(asm)], capture_output=True, check=True)
+        code = [line.split(";")[0].strip() for line in asm.read_text().splitlines()]
+        code = [line for line in code if line and not line.startswith(".") and not line.endswith(":")]
+        for i, line in enumerate(code):
+            if re.search(r"\bm0\b", line):
+                # an m0 write of a copy helper, directly followed by its copy
+                assert setter.match(line) and code[i + 1].startswith("global_load_lds_dword"), \
+                    f"{os.path.basename(src)}: m0 used outside the copies: {line!r}, then {code[i + 1]!r}"
