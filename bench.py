@@ -10,11 +10,14 @@ Timing: each workload first runs untimed, back to back, for at least 50 ms and 1
 ~20-25 ms of load to leave its idle state), then its warm-up steps; the timed steps run back to back between two HIP events on torch's current stream
 (the stream the library launches on); `roofline.achieved` = algorithmic work / mean time per step. Kernels shorter than ~50 us are timed by replaying a
 captured HIP graph of many launches, so host launch overhead does not stretch them. HBM-bound kernels rotate over
-more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve them. The CPU baseline is the
-reference's attention fallback (attention_bmm: chunked baddbmm -> softmax -> bmm, attention.py:15-43) on the host
-cores over a bounded sample.
+more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve them.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME]
+CPU baselines: every workload carries one -- the reference's own torch fallback for it (oracle/cpu_baseline.py: the
+dequantized matmul after a dense ConvRot for the linears, attention_bmm for attention, the fp32 cast RMSNorm, fp32
+decode attention, the unfused block), timed on the host cores on the same seeded inputs or a stated sample of them,
+with the host's CPU model, logical CPU count and torch thread count under "host".
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME] [--cpu-only]
 
 "decode_layer" times one token through one Qwen3-8B-shaped layer's int8 linears and decode attention, and
 "dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192, 4096 tokens).
@@ -48,6 +51,7 @@ def parse():
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default=None)
+    ap.add_argument("--cpu-only", action="store_true", help="time only the CPU baselines (no GPU needed)")
     return ap.parse_args()
 
 
@@ -363,6 +367,11 @@ WORKLOADS = {
     "copy": w_copy,
 }
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}
+# The roofline of each workload (the 4th item its function returns), for the CPU leg, which runs without a GPU.
+WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
+                  "w4a8_gemm": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
+                  "decode_gemv_n1024": "hbm", "decode_gemv_n12288": "hbm", "decode_attention": "hbm", "decode_layer": "hbm", "dit_block": "mfma_i8",
+                  "copy": "hbm"}
 
 
 def run_workload(torch, dev, name, steps, warmup, traffic):
@@ -376,31 +385,187 @@ def run_workload(torch, dev, name, steps, warmup, traffic):
     return rec
 
 
-def cpu_baseline(torch, q, k, v, seconds=10.0):
-    """The reference's attention fallback on the host cores. fp32: the whole workload (all 24 heads at full length),
-    repeated until about `seconds` of CPU time; fp16: one head with 1024 of its query rows (torch's CPU fp16 matmul is
-    far slower), bounded to about 3 s. The faster rate is reported, as total FLOP over total time."""
-    import oracle
-    threads = torch.get_num_threads()
-    H, S, D = q.shape[1], q.shape[2], q.shape[3]
-    best = None
-    for dtype, heads, rows, budget in ((torch.float32, H, S, seconds), (torch.float16, 1, 1024, 3.0)):
-        qs = q[:, :heads, :rows].to(dtype).contiguous()
-        ks, vs = (t[:, :heads].to(dtype).contiguous() for t in (k, v))
-        oracle.attention_bmm_cpu(qs[:, :1, :128], ks[:, :1], vs[:, :1], 128 ** -0.5)  # warm-up
-        runs, elapsed = 0, 0.0
-        while elapsed < budget:
-            t0 = time.perf_counter()
-            oracle.attention_bmm_cpu(qs, ks, vs, 128 ** -0.5)
-            elapsed += time.perf_counter() - t0
-            runs += 1
-        rate = 4.0 * heads * rows * S * D * runs / elapsed / 1e12
-        log(f"cpu attention_bmm {dtype}: {rate:.4f} TFLOP/s ({heads} heads x {rows} rows, {runs} runs in {elapsed:.1f} s)")
-        if best is None or rate > best[0]:
-            best = (rate, str(dtype).replace("torch.", ""), heads, rows, runs, elapsed)
-    return {"value": round(best[0], 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"attention_bmm (chunked baddbmm/softmax/bmm in {best[1]}) over {best[2]} of 24 heads x {best[3]} query rows, "
-                      f"S=4096, D=128, {best[4]} runs in {best[5]:.1f} s after a warm-up; {os.cpu_count()} logical CPUs visible"}
+# --------------------------------------------------------------------------------------------------- CPU baselines
+# The reference's own torch fallback for each workload (oracle/cpu_baseline.py), on the host cores, on the same seeded
+# inputs (generated on the CPU with the workload's seeds) or a bounded sample of them. Each returns (callable, work,
+# sample): work in the unit of the GPU workload's roofline (ops or bytes) for what one call computes.
+
+def _cpu_w8a8(torch):
+    g = gen(torch, 1)
+    M, K, N = 4096, 3072, 3072
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:8]] *= 30
+    x = x.half().float()
+    w = torch.randint(-127, 128, (N, K), generator=gen(torch, 2), dtype=torch.int8)
+    ws = (torch.rand(N, generator=gen(torch, 3)) * 2e-3 + 1e-3).float()
+    return M, K, N, x, w, ws
+
+
+def c_attention(torch, heads=2):
+    from oracle import cpu_baseline as cb
+    q, k, v = (t[:, :heads].float().contiguous() for t in attention_inputs(torch))
+    return (lambda: cb.attention_bmm(q, k, v, 128 ** -0.5)), ATTN_FLOP * heads / 24, \
+        f"attention_bmm (attention.py:15-43) in fp32 over {heads} of the 24 heads, S=4096, D=128"
+
+
+def c_w8a8_gemm(torch):
+    from oracle import cpu_baseline as cb
+    M, K, N, x, w, ws = _cpu_w8a8(torch)
+    xr = cb.rotate(x, 128)
+    return (lambda: cb.linear_dequant(xr, w, ws)), 2.0 * M * N * K, "F.linear(x_rot, W.float() * ws) (int8_gemv.py:58-59), fp32, the full 4096x3072x3072"
+
+
+def c_w8a8_linear(torch):
+    from oracle import cpu_baseline as cb
+    M, K, N, x, w, ws = _cpu_w8a8(torch)
+    H = cb.hadamard(128)
+    return (lambda: cb.w8a8_linear(x, w, ws, 128, H)), 2.0 * M * N * K, "dense group-128 ConvRot + F.linear(x_rot, W.float() * ws), fp32, full size"
+
+
+def c_w8a8_rot_quant(torch):
+    from oracle import cpu_baseline as cb
+    M, K, N, x, w, ws = _cpu_w8a8(torch)
+    H = cb.hadamard(128)
+    return (lambda: cb.rot_quant(x, 128, H)), M * K * 2 + M * K + M * 4, "dense group-128 ConvRot + per-token int8 quantization in torch, fp32, full size"
+
+
+def c_w4a8_gemm(torch):
+    from oracle import cpu_baseline as cb
+    M, K, N, x, _, _ = _cpu_w8a8(torch)
+    N = 12288
+    w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 8), dtype=torch.uint8)
+    gs = (torch.rand(N, K // 128, generator=gen(torch, 9)) * 1.5e-2 + 5e-3).half()
+    xr = cb.rotate(x, 256)
+    return (lambda: cb.linear_w4_dequant(xr, w4, gs)), 2.0 * M * N * K, \
+        "int4 unpacked, group-128 scales applied, F.linear in fp32, the full 4096x12288x3072"
+
+
+def c_mlp_rms_norm(torch):
+    from oracle import cpu_baseline as cb
+    M, K = 4096, 3072
+    h = torch.randn(1, M, K, generator=gen(torch, 10)).half()
+    w = (torch.randn(K, generator=gen(torch, 11)) * 0.1).float()
+    return (lambda: cb.rms_norm(h, w, 1e-6)), M * K * 4 + K * 4, "fp32 cast RMSNorm (x.float(), normalise, * (w + 1), .half()), full 4096x3072"
+
+
+def c_mlp_swiglu_rot_quant(torch):
+    from oracle import cpu_baseline as cb
+    M, F = 4096, 8192
+    gt = torch.randn(M, F, generator=gen(torch, 12)).half()
+    up = torch.randn(M, F, generator=gen(torch, 13)).half()
+    H = cb.hadamard(256)
+    return (lambda: cb.swiglu_rot_quant(gt, up, 256, H)), M * F * 4 + M * F + M * 4, \
+        "F.silu(gate).mul_(up) in fp16, dense ConvRot (fp32), per-token int8, full 4096x8192"
+
+
+def c_mlp_down_gemm(torch):
+    from oracle import cpu_baseline as cb
+    M, F, N = 4096, 8192, 3072
+    a = torch.randn(M, F, generator=gen(torch, 12))
+    w = torch.randint(-127, 128, (N, F), generator=gen(torch, 14), dtype=torch.int8)
+    ws = (torch.rand(N, generator=gen(torch, 15)) * 2e-3 + 1e-3).float()
+    return (lambda: cb.linear_dequant(a, w, ws)), 2.0 * M * N * F, "F.linear(a, W.float() * ws), fp32, the full 4096x3072x8192"
+
+
+def c_decode_gemv(torch, N):
+    from oracle import cpu_baseline as cb
+    K = 4096
+    x = torch.randn(1, K, generator=gen(torch, 16))
+    w = torch.randint(-127, 128, (N, K), generator=gen(torch, 17), dtype=torch.int8)
+    s = (torch.rand(N, generator=gen(torch, 18)) * 2e-3 + 1e-3).float()
+    return (lambda: cb.gemv(x, w, s)), N * K + N * 4 + K * 2 + N * 2, \
+        f"F.linear(x, W.float() * scale) (int8_gemv.py:58-59) for one fp32 token, K=4096, N={N}"
+
+
+def c_decode_attention(torch):
+    from oracle import cpu_baseline as cb
+    cap, H, Hkv = 2048, 32, 8
+    q = torch.randn(1, 1, H, 128, generator=gen(torch, 19))
+    k = torch.randn(1, cap, Hkv, 128, generator=gen(torch, 20))
+    v = torch.randn(1, cap, Hkv, 128, generator=gen(torch, 21))
+    return (lambda: cb.attention_decode(q, k, v, cap)), 2 * cap * Hkv * 512 + 2 * H * 512, \
+        "fp32 softmax(q K^T / sqrt(128)) V, 32 query / 8 KV heads, 2048 positions"
+
+
+def c_decode_layer(torch):
+    from oracle import cpu_baseline as cb
+    D, Hq, Hkv, F, cap = 4096, 32, 8, 12288, 2048
+    shapes = {"q": (D, D), "k": (Hkv * 128, D), "v": (Hkv * 128, D), "o": (D, D), "gate": (F, D), "up": (F, D), "down": (D, F)}
+    g = gen(torch, 40)
+    w = {n: torch.randint(-127, 128, shp, generator=g, dtype=torch.int8) for n, shp in shapes.items()}
+    s = {n: (torch.rand(shp[0], generator=g) * 2e-3 + 1e-3).float() for n, shp in shapes.items()}
+    kc, vc = (torch.randn(1, cap, Hkv, 128, generator=g) for _ in range(2))
+    x = torch.randn(1, 1, D, generator=g)
+    H = cb.hadamard(256)
+    work = sum(n * k for n, k in shapes.values()) + 4 * sum(n for n, _ in shapes.values()) + 2 * cap * Hkv * 512 + 4 * (D * 10 + Hkv * 256 + F * 4)
+    return (lambda: cb.decode_layer(x, w, s, kc, vc, cap, Hq, 256, H)), work, \
+        "seven ConvRot + dequantized single-token linears and fp32 decode attention of one Qwen3-8B-shaped layer"
+
+
+def c_dit_block(torch, L=1024):
+    from oracle import cpu_baseline as cb
+    D, heads, hidden = 3072, 24, 8192
+    g = gen(torch, 20)
+    blk = {"eps": 1e-6}
+    for n, (o, i) in {"q": (D, D), "k": (D, D), "v": (D, D), "gate": (D, D), "o": (D, D), "gate_mlp": (hidden, D), "up": (hidden, D),
+                      "down": (D, hidden)}.items():
+        blk["w_" + n] = torch.randint(-127, 128, (o, i), generator=g, dtype=torch.int8)
+        blk["s_" + n] = (torch.rand(o, generator=g) * 2e-3 + 1e-3).float()
+    for n, d in (("prenorm", D), ("postnorm", D), ("qnorm", 128), ("knorm", 128)):
+        blk[n] = torch.randn(d, generator=g) * 0.1
+    blk["mod"] = [torch.randn(1, 1, D, generator=g) * 0.2 for _ in range(6)]
+    x = torch.randn(1, L, D, generator=gen(torch, 21))
+    ang = torch.randn(1, 1, L, 64, generator=gen(torch, 22))
+    freqs = torch.stack([torch.cos(ang), -torch.sin(ang), torch.sin(ang), torch.cos(ang)], -1).reshape(1, 1, L, 64, 2, 2)
+    H = cb.hadamard(256)
+    work = 5 * 2.0 * L * D * D + 3 * 2.0 * L * D * hidden + 2 * 4.0 * heads * L * L * 128
+    return (lambda: cb.block(x, blk, freqs, 256, H)), work, \
+        f"the unfused Krea 2 block in fp32 (dequantized ConvRot linears, attention_bmm, fp32 norms) over {L} of the 4096 tokens"
+
+
+CPU_BASELINES = {
+    "attention_f16": c_attention,
+    "attention_i8qk": c_attention,
+    "w8a8_gemm": c_w8a8_gemm,
+    "w8a8_rot_quant": c_w8a8_rot_quant,
+    "w8a8_linear": c_w8a8_linear,
+    "w4a8_gemm": c_w4a8_gemm,
+    "mlp_rms_norm": c_mlp_rms_norm,
+    "mlp_swiglu_rot_quant": c_mlp_swiglu_rot_quant,
+    "mlp_down_gemm": c_mlp_down_gemm,
+    "decode_gemv_n4096": lambda t: c_decode_gemv(t, 4096),
+    "decode_gemv_n1024": lambda t: c_decode_gemv(t, 1024),
+    "decode_gemv_n12288": lambda t: c_decode_gemv(t, 12288),
+    "decode_attention": c_decode_attention,
+    "decode_layer": c_decode_layer,
+    "dit_block": c_dit_block,
+}
+
+
+def cpu_baseline(torch, name, seconds=1.5, **kw):
+    """Times the CPU fallback of workload `name` on the host cores: calls back to back until `seconds` have passed (at
+    least one); a first call shorter than a quarter of the budget is a discarded warm-up. Rate = work / mean time."""
+    fn, work, sample = CPU_BASELINES[name](torch, **kw)
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    runs, elapsed = (0, 0.0) if first < seconds / 4 else (1, first)
+    while elapsed < seconds or runs == 0:
+        t0 = time.perf_counter()
+        fn()
+        elapsed += time.perf_counter() - t0
+        runs += 1
+    kind = PEAKS[WORKLOAD_BOUND[name]][0]
+    rate = work / (elapsed / runs) / (1e12 if kind == "mfma" else 1e9)
+    unit = "GB/s" if kind == "hbm" else "TOP/s" if WORKLOAD_BOUND[name] == "mfma_i8" else "TFLOP/s"
+    log(f"cpu {name}: {rate:.4g} {unit} ({runs} runs, {elapsed / runs * 1e3:.1f} ms each)")
+    return {"value": round(rate, 5), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{sample}; {runs} timed runs, {elapsed / runs * 1e3:.2f} ms each"}
+
+
+def host_info(torch):
+    from oracle import cpu_baseline as cb
+    return {"cpu_model": cb.cpu_model(), "logical_cpus": os.cpu_count(), "torch_threads": torch.get_num_threads()}
 
 
 def main():
@@ -410,6 +575,10 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.cpu_only:
+        names = [args.only] if args.only else list(CPU_BASELINES)
+        print(json.dumps({"host": host_info(torch), **{n: cpu_baseline(torch, n) for n in names}}), flush=True)
+        return
     import __graft_entry__
     __graft_entry__.load_package()
     dev = torch.device("cuda:0")
@@ -443,7 +612,11 @@ def main():
         result["components"] = {name: run_workload(torch, dev, name, args.steps, args.warmup, traffic)
                                 for name in WORKLOADS if name not in ("attention_f16", "copy")}
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(torch, *attention_inputs(torch))
+        # The headline's sample is larger (6 of 24 heads, about 10 s); each component's is about 1.5 s.
+        result["cpu_baseline"] = cpu_baseline(torch, "attention_f16", seconds=10.0, heads=6)
+        result["host"] = host_info(torch)
+        for name, rec in result.get("components", {}).items():
+            rec["cpu_baseline"] = cpu_baseline(torch, name)
     print(json.dumps(result), flush=True)
 
 

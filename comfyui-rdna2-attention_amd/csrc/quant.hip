@@ -21,6 +21,7 @@ struct ModArgs {
 };
 
 #define QT 256  // threads per row of the reference's kernels (rms_norm's summation order follows it)
+#define MAX_LDS_K 16384  // longest row held in LDS (fp16, 32 KiB); rotations need it, plain quantization does not
 
 // int8_gemm.hip:106-109
 // s - 2 x as one FMA: 2 x is exact, so fma(-2, x, s) rounds s - 2 x once, exactly as the separate product and
@@ -108,10 +109,13 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
     const half_t* x = X + (size_t)row * ldx;
     float mx = 0.f;
 
+    // GROUP 0 stages the row in LDS when it fits (K <= MAX_LDS_K); longer rows are read again from global memory by
+    // the quantization pass below, so quant_pack_a takes any K, as the reference's does.
+    const bool staged = GROUP != 0 || K <= MAX_LDS_K;
     if constexpr (GROUP == 0) {
         for (int i = t; i < K / 8; i += NW * 64) {
             const h8 v = ((const h8*)x)[i];
-            ((h8*)rotated)[i] = v;
+            if (staged) ((h8*)rotated)[i] = v;
 #pragma unroll
             for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf((float)v[j]));
         }
@@ -289,8 +293,9 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
 
     const float rcp = 1.f / scale;
     int8_t* out = Aq + (size_t)row * K;
+    const h8* src = staged ? (const h8*)rotated : (const h8*)x;
     for (int ch = t; ch < K / 16; ch += NW * 64) {
-        const h8 lo = ((const h8*)rotated)[ch * 2], hi = ((const h8*)rotated)[ch * 2 + 1];
+        const h8 lo = src[ch * 2], hi = src[ch * 2 + 1];
         int q[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
 
 template <int ACT, bool I4, int GROUP, int NW>
 static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
-    const size_t lds = (size_t)K * 2 + (GROUP ? NW * 64 * 17 * sizeof(float) : 0);
+    const size_t lds = GROUP ? (size_t)K * 2 + NW * 64 * 17 * sizeof(float) : K <= MAX_LDS_K ? (size_t)K * 2 : 0;
     hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
                        (const half_t*)u, (int8_t*)aq, as, K, mod);
     return (int)hipGetLastError();
@@ -316,7 +321,7 @@ static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq,
 
 template <int ACT, bool I4, int GROUP>
 static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
-    if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || K > 16384) return RDA_ERR_INVALID;
+    if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || (GROUP != 0 && K > MAX_LDS_K)) return RDA_ERR_INVALID;
     if constexpr (ACT == MOD || GROUP == 0) {
         return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
     } else {

@@ -61,12 +61,24 @@ def quantized(M, row_bytes, device):
             torch.empty(M, dtype=torch.float32, device=device))
 
 
+def _rows(x):
+    """x as rows the quantization kernels can address by a row pitch: contiguous last dimension, rows not overlapping."""
+    if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) < x.shape[1]):
+        return x.contiguous()
+    return x
+
+
 def quantize(quant, x, K, up=None, group=ROT_GROUP):
-    """Runs one activation -> rotate -> quantize entry point. x is (M, K) fp16, or (M, 2K) for situ. Returns (packed, scales)."""
+    """Runs one activation -> rotate -> quantize entry point. x is (M, K) fp16, or (M, 2K) for situ; any strides
+    (layouts the kernels cannot address are copied first). Returns (packed, scales)."""
     k = get_kernels()
     M = x.shape[0]
     packed_a, a_scale = quantized(M, K, x.device)
     p = _lib.ptr
+    if quant is k.swiglu_rot_quant_pack_a or quant is k.gate_rot_quant_pack_a:  # both operands at a pitch of K
+        x, up = x.contiguous(), up.contiguous()
+    else:
+        x = _rows(x)
     if quant is k.quant_pack_a:
         launch(quant, M, 1, ROT_THREADS, [p(x), x.stride(0), p(packed_a), p(a_scale), M, K])
     elif quant is k.swiglu_rot_quant_pack_a or quant is k.gate_rot_quant_pack_a:
@@ -270,6 +282,7 @@ def quantize_block_input(x, norm, scale, shift):
     global shared
     B, L, K = x.shape
     packed_a, a_scale = quantized(B * L, K, x.device)
+    x = x.contiguous()  # read at a row pitch of K
     weight = comfy.model_management.cast_to(norm.scale, dtype=torch.float32, device=x.device)
     s, t = (1 + scale).contiguous(), shift.contiguous()
     p = _lib.ptr

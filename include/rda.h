@@ -25,9 +25,11 @@ int rda_version(void);
 
 /* ------------------------------------------------------------------ linear path ---------- */
 /* Activations: x fp16 rows of K values at a pitch of ldx elements. Outputs: a_q int8 [M, K]
- * row-major, a_scale fp32 [M]. K must be a multiple of group (256 or 128) and <= 16384. */
+ * row-major, a_scale fp32 [M]. With a rotation, K must be a multiple of group (256 or 128) and
+ * <= 16384 (the rotated row is held in LDS). */
 
-/* quant_pack_a, int8_gemm.py:67 (kernel int8_gemm.hip:93-103): per-row absmax int8, no rotation. */
+/* quant_pack_a, int8_gemm.py:67 (kernel int8_gemm.hip:93-103): per-row absmax int8, no rotation.
+ * Any K that is a multiple of 16. */
 int rda_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, void* stream);
 
 /* rot_quant_pack_a, int8_gemm.py:67 (int8_gemm.hip:245-247): block Hadamard + per-row int8. */

@@ -36,33 +36,40 @@ def build():
     subprocess.run(["make", "-s", "-C", HERE], check=True)
 
 
+def load(path):
+    """A build of rda_oracle.c at `path`, with its entry points' C signatures declared."""
+    L = ctypes.CDLL(path)
+    f32, i32, u16, i64 = ctypes.c_float, ctypes.c_int, ctypes.c_uint16, ctypes.c_long
+    p = ctypes.c_void_p
+    L.orc_expf.restype = f32
+    L.orc_expf.argtypes = [f32]
+    L.orc_exp2f.restype = f32
+    L.orc_exp2f.argtypes = [f32]
+    L.orc_h2f.restype = f32
+    L.orc_h2f.argtypes = [u16]
+    L.orc_f2h.restype = u16
+    L.orc_f2h.argtypes = [f32]
+    for name in ("orc_swiglu", "orc_sigmoid_gate", "orc_situ"):
+        getattr(L, name).restype = f32
+        getattr(L, name).argtypes = [f32, f32]
+    L.orc_modulate.restype = f32
+    L.orc_modulate.argtypes = [f32, f32, f32, f32, f32]
+    L.orc_quant_rows.argtypes = [i32, i32, p, i32, p, p]
+    L.orc_rot_quant_rows.argtypes = [i32, i32, i32, i32, i32, p, i32, p, p, p, p, i32, f32, p, p, p]
+    L.orc_gemm_epilogue.argtypes = [i32, i32, p, p, p, p, p, p, i32, p]
+    L.orc_w4a8_epilogue.argtypes = [i32, i32, i32, p, p, p, p, p]
+    L.orc_rms_norm.argtypes = [i32, i32, i32, i32, p, i64, i64, i64, p, f32, p, i64, p]
+    L.orc_rotate_f32.argtypes = [i32, i32, p, p]
+    L.orc_quant_rows_rint.argtypes = [i32, i32, p, i64, p, p]
+    return L
+
+
 def lib():
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        L = ctypes.CDLL(LIB_PATH)
-        f32, i32, u16, i64 = ctypes.c_float, ctypes.c_int, ctypes.c_uint16, ctypes.c_long
-        p = ctypes.c_void_p
-        L.orc_expf.restype = f32
-        L.orc_expf.argtypes = [f32]
-        L.orc_exp2f.restype = f32
-        L.orc_exp2f.argtypes = [f32]
-        L.orc_h2f.restype = f32
-        L.orc_h2f.argtypes = [u16]
-        L.orc_f2h.restype = u16
-        L.orc_f2h.argtypes = [f32]
-        for name in ("orc_swiglu", "orc_sigmoid_gate", "orc_situ"):
-            getattr(L, name).restype = f32
-            getattr(L, name).argtypes = [f32, f32]
-        L.orc_quant_rows.argtypes = [i32, i32, p, i32, p, p]
-        L.orc_rot_quant_rows.argtypes = [i32, i32, i32, i32, i32, p, i32, p, p, p, p, i32, f32, p, p, p]
-        L.orc_gemm_epilogue.argtypes = [i32, i32, p, p, p, p, p, p, i32, p]
-        L.orc_w4a8_epilogue.argtypes = [i32, i32, i32, p, p, p, p, p]
-        L.orc_rms_norm.argtypes = [i32, i32, i32, i32, p, i64, i64, i64, p, f32, p, i64, p]
-        L.orc_rotate_f32.argtypes = [i32, i32, p, p]
-        L.orc_quant_rows_rint.argtypes = [i32, i32, p, i64, p, p]
-        _lib = L
+        _lib = load(LIB_PATH)
     return _lib
 
 
@@ -358,23 +365,3 @@ def attention_faithful(q, k, v, scale, block=16, threshold=8.0):
             out[b, h] = (o * (np.float32(1) / l)[:, None]).astype(np.float16)
     return out
 
-
-def attention_bmm_cpu(q, k, v, scale, chunk_bytes=128 * 1024 * 1024):
-    """The reference's fallback (attention.py:15-43) with torch on the CPU: per chunk of heads,
-    baddbmm(beta=0, alpha=scale) -> softmax -> bmm. q/k/v torch tensors (B, H, L, D). CPU-baseline only."""
-    import torch
-    b, heads, q_len, d = q.shape
-    k_len = k.shape[2]
-    batch = b * heads
-    q = q.reshape(batch, q_len, d).contiguous()
-    k = k.reshape(batch, k_len, d).contiguous().transpose(1, 2).contiguous()
-    v = v.reshape(batch, k_len, -1)
-    out = torch.empty((batch, q_len, v.shape[-1]), dtype=q.dtype)
-    step = min(batch, max(1, chunk_bytes // (q_len * k_len * q.element_size())))
-    scores = torch.empty((step, q_len, k_len), dtype=q.dtype)
-    for i in range(0, batch, step):
-        s = scores[:min(step, batch - i)]
-        torch.baddbmm(s, q[i:i + step], k[i:i + step], beta=0, alpha=scale, out=s)
-        torch.softmax(s, -1, out=s)
-        torch.bmm(s, v[i:i + step], out=out[i:i + step])
-    return out.view(b, heads, q_len, -1)

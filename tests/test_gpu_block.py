@@ -6,7 +6,7 @@ of the oracle's stages -- modulated RMSNorm + rotation + quantization, the GEMM 
 QK-norm + rope, sigmoid-gate and SwiGLU quantization -- in the order and with the roundings of the reference's fused
 path. Attention is the one stage whose kernel is tolerance-tested rather than bit-exact, so the chain runs the
 attention kernel on the oracle's own q, k, v: from there on every stage is exact, and the block must agree bit for
-bit. A second check puts the float64 attention in the chain and bounds the whole block's deviation."""
+bit. (The attention kernel itself is checked against float64 softmax in tests/test_gpu_attention.py.)"""
 import numpy as np
 import pytest
 import torch
@@ -87,20 +87,3 @@ def test_block_forward_matches_oracle_chain(dev, hooked, B, L, D, heads, hidden,
     ref = oracle_block(blk, x, freqs, gpu_attention)
     assert_same(bits(out), bits(ref))
 
-
-def test_block_forward_tracks_float64_attention(dev, hooked):
-    """With the float64 attention in the chain, the block's output tracks it: relative to each output row's
-    magnitude, the mean |out - ref| stays <= 0.2% and the largest <= 5%. The bound is empirical (measured: mean
-    0.08%, max 2.7%): the int8 grids downstream of attention turn its fp16-level differences into occasional
-    one-step code changes, whose effect on a row depends on the weights they meet. The bit-exact test above is the
-    parity check; this one guards the whole block against a drift that an exact chain could share."""
-    B, L, D, heads, hidden = 1, 512, 256, 2, 512
-    blk = fakes.make_krea2_block(hooked, D, heads, hidden, B, dev, seed=11)
-    x = torch.randn(B, L, D, generator=gen(12)).half()
-    freqs = freqs_for(L, 13)
-    out = int8_gemm.block_forward(blk, False, x.to(dev), None, freqs.to(dev)).cpu().double().numpy()
-    ref = oracle_block(blk, x, freqs, lambda q, k, v: oracle.attention_f64(q, k, v, 128 ** -0.5).astype(np.float16)).astype(np.float64)
-    row = np.abs(ref).max(axis=-1, keepdims=True)
-    rel = np.abs(out - ref) / row
-    print(f"block vs float64 attention: max rel {rel.max():.2e}, mean rel {rel.mean():.2e}", flush=True)
-    assert rel.mean() <= 2e-3 and rel.max() <= 0.05

@@ -26,7 +26,7 @@ def test_rot_quant_bit_exact(dev, M, K, group):
     assert_same(q_of(packed, M, K), q_ref)
 
 
-@pytest.mark.parametrize("M,K", [(3, 64), (100, 3072), (9, 16384)])
+@pytest.mark.parametrize("M,K", [(3, 64), (100, 3072), (9, 16384), (5, 18432), (4, 24576)])  # rows past 16384 are re-read, not staged
 def test_quant_pack_a_bit_exact(dev, M, K):
     print(f"quant_pack_a M={M} K={K}", flush=True)
     x = activations(M, K, seed=3)
@@ -162,7 +162,8 @@ def test_w8a8_linear_bit_exact(dev, M, N, K, group, bias):
     assert_same(bits(out), bits(ref))
 
 
-@pytest.mark.parametrize("B,L,K,N", [(2, 300, 512, 256), (1, 600, 256, 576), (2, 2048, 256, 8192)])  # 128-, 192- and 256-wide tiles
+# 128-, 192- and 256-wide tiles of the direct-copy GEMM; N = 320 (no such width divides it) takes the register-load GEMM
+@pytest.mark.parametrize("B,L,K,N", [(2, 300, 512, 256), (1, 600, 256, 576), (2, 2048, 256, 8192), (1, 520, 256, 320)])
 def test_gemm_residual_epilogue_bit_exact(dev, B, L, K, N):
     print(f"residual epilogue B={B} L={L} K={K} N={N}", flush=True)
     M = B * L
@@ -251,3 +252,53 @@ def test_w8a8_linear_unaligned_weight_view(dev):
     out = int8_gemm.linear(x.to(dev), wu, ws.to(dev), None, rotate=True)
     q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
     assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())))
+
+
+def test_plain_int8_linear_long_rows(dev):
+    """A non-rotated int8 linear (quant_pack_a + GEMM, the path of any eligible int8 layer without ConvRot) with
+    K = 18432, past the rows the quantization pass holds in LDS: bit-exact, as the reference takes any K here."""
+    M, N, K = 520, 128, 18432
+    x = activations(M, K, seed=41)
+    w = int8_weights(N, K, seed=42)
+    ws = channel_scales(N, seed=43)
+    out = int8_gemm.linear(x.to(dev), w.to(dev), ws.to(dev), None)
+    q_ref, s_ref = oracle.quant_rows(x.numpy())
+    assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())))
+
+
+# Scale groups of 64 and 256 are served by the register-load GEMM's per-group fold; 128 by the direct-copy kernel.
+@pytest.mark.parametrize("scale_group", [64, 256])
+def test_w4a8_other_scale_groups_bit_exact(dev, scale_group):
+    M, N, K = 520, 256, 1024
+    print(f"w4a8 scale_group={scale_group} M={M} N={N} K={K}", flush=True)
+    x = activations(M, K, seed=51, outliers=0)
+    w, wp = int4_weights(N, K, seed=52)
+    gs = (torch.rand(N, K // scale_group, generator=gen(53)) * 1.5e-2 + 5e-3).half()
+    out = int8_gemm.linear_w4a8(x.to(dev), wp.to(dev), gs.to(dev), scale_group=scale_group)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    ref = oracle.w4a8_epilogue(oracle.w4a8_partials(q_ref, w.numpy(), group=scale_group), s_ref, gs.numpy())
+    assert_same(bits(out), bits(ref))
+
+
+@pytest.mark.parametrize("layout", ["every_other_column", "transposed"])
+def test_linears_take_strided_activations(dev, layout):
+    """Activations whose last dimension is not contiguous are copied into rows before the quantization pass: the
+    W4A8 and W8A8 linears give the results of the contiguous input."""
+    M, N, K = 512, 256, 1024
+    x = activations(M, K, seed=61, outliers=0)
+    if layout == "every_other_column":
+        big = torch.zeros(M, 2 * K, dtype=torch.float16, device=dev)
+        big[:, ::2] = x.to(dev)
+        xv = big[:, ::2]
+    else:
+        xv = x.t().contiguous().to(dev).t()
+    assert xv.stride(-1) != 1
+    w, wp = int4_weights(N, K, seed=62)
+    gs = (torch.rand(N, K // 128, generator=gen(63)) * 1.5e-2 + 5e-3).half()
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    out = int8_gemm.linear_w4a8(xv, wp.to(dev), gs.to(dev))
+    assert_same(bits(out), bits(oracle.w4a8_epilogue(oracle.w4a8_partials(q_ref, w.numpy()), s_ref, gs.numpy())))
+    w8 = int8_weights(N, K, seed=64)
+    ws = channel_scales(N, seed=65)
+    out = int8_gemm.linear(xv, w8.to(dev), ws.to(dev), None, rotate=True)
+    assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w8.numpy()), s_ref, ws.numpy())))

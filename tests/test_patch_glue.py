@@ -1,0 +1,437 @@
+"""The model-patch glue and the node shim on the CPU, with stand-ins for the ComfyUI objects they touch: which object
+patches each patch() installs (and on which modules it does not), the fallbacks each patched forward takes, the
+generate() scope, the merged gate/up prefill of mlp_forward, and RDNA2Attention.execute / RDNA2TextGenerate.execute
+with relayout_weights (reference: int8_gemv.py:67-148, rms_norm.py:61-64, int8_gemm.py:160-173, 229-232,
+__init__.py:22-93)."""
+import importlib.util
+import logging
+import sys
+import types
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import __graft_entry__
+from comfyui_rdna2_attention_amd import int8_gemm, int8_gemv, rms_norm
+
+
+class Patcher:
+    """Records add_object_patch calls; model holds the module tree."""
+
+    def __init__(self, model):
+        self.model, self.patches, self.callbacks = model, {}, []
+
+    def add_object_patch(self, name, obj):
+        self.patches[name] = obj
+
+    def get_model_object(self, name):
+        return getattr(self.model, name)
+
+
+def named(root, tree):
+    """A module tree whose named_modules() yields `tree` (name -> module) under `root`."""
+    root.named_modules = lambda: [("", root), *tree.items()]
+    return root
+
+
+# ----------------------------------------------------------------------------------------------- int8_gemv.patch
+
+class MixedPrecisionOp:
+    pass
+
+
+class Linear(MixedPrecisionOp):
+    def __init__(self, N, K, fmt="int8_tensorwise", scale_n=None, scale_dtype=torch.float32, transposed=False, convrot=False, group=256):
+        self.quant_format = fmt
+        self.weight = types.SimpleNamespace(shape=(N, K), dtype=torch.int8, _params=types.SimpleNamespace(
+            scale=torch.ones(scale_n or N, dtype=scale_dtype), transposed=transposed, convrot=convrot, convrot_groupsize=group))
+        self.weight_function = self.bias_function = None
+
+
+class MLP:
+    def __init__(self, merged=False):
+        self.merged_mlp = merged
+        self.gate_proj, self.up_proj = Linear(64, 512), Linear(64, 512)
+
+
+class BaseQwen3:
+    def __init__(self, lm_head=False, fixed_kv=True, heads=32, kv_heads=8, head_dim=128, embed_dtype=torch.bfloat16, vocab=1024, hidden=512):
+        cfg = types.SimpleNamespace(lm_head=lm_head, head_dim=head_dim, num_attention_heads=heads, num_key_value_heads=kv_heads)
+        embed = types.SimpleNamespace(weight=torch.zeros(vocab, hidden, dtype=embed_dtype))
+        self.model = types.SimpleNamespace(config=cfg, fixed_kv=fixed_kv, embed_tokens=embed)
+
+
+@pytest.fixture
+def gemv_fakes(monkeypatch):
+    kitchen = types.SimpleNamespace(flash_attention_decode="kitchen-original")
+    monkeypatch.setattr(int8_gemv, "comfy_kitchen", kitchen)
+    monkeypatch.setattr(int8_gemv, "MixedPrecisionOp", MixedPrecisionOp)
+    monkeypatch.setattr(int8_gemv, "MLP", MLP)
+    monkeypatch.setattr(int8_gemv, "BaseQwen3", BaseQwen3)
+    return kitchen
+
+
+def test_int8_gemv_patch_installs_eligible_objects(gemv_fakes):
+    tree = {
+        "ok": Linear(4096, 4096, convrot=True, group=256),
+        "ok_plain": Linear(1024, 512),
+        "bad_rows": Linear(4100, 512),  # N % 16
+        "bad_k": Linear(64, 500),  # K % 512
+        "bad_scale_count": Linear(64, 512, scale_n=1),
+        "bad_scale_dtype": Linear(64, 512, scale_dtype=torch.float16),
+        "bad_transposed": Linear(64, 512, transposed=True),
+        "bad_format": Linear(64, 512, fmt="float8"),
+        "mlp": MLP(),
+        "mlp_merged": MLP(merged=True),
+        "qwen": BaseQwen3(),
+        "qwen_lm_head": BaseQwen3(lm_head=True),
+    }
+    clip = types.SimpleNamespace(patcher=Patcher(named(types.SimpleNamespace(), tree)))
+    int8_gemv.patch(clip)
+    p = clip.patcher.patches
+    assert set(p) == {"ok.forward", "ok_plain.forward", "mlp.forward", "qwen.logits", "qwen.generate", "qwen.model.init_kv_cache"}
+    assert p["ok.forward"].func is int8_gemv.linear_forward and p["ok.forward"].args == (tree["ok"], 4096, 4096, torch.int8, 256)
+    assert p["ok_plain.forward"].args[-1] == 0  # no ConvRot: group 0
+    assert p["mlp.forward"].func is int8_gemv.mlp_forward and p["mlp.forward"].args == (tree["mlp"], torch.int8)
+    assert p["qwen.logits"].func is int8_gemv.logits and p["qwen.generate"].func is int8_gemv.generate
+    assert p["qwen.model.init_kv_cache"].func is int8_gemv.init_kv_cache
+    assert gemv_fakes.flash_attention_decode is int8_gemv.attention_decode
+
+
+@pytest.mark.parametrize("kw", [{"fixed_kv": False}, {"head_dim": 64}, {"heads": 16}])
+def test_int8_gemv_patch_keeps_kitchen_decode_when_ineligible(gemv_fakes, kw):
+    clip = types.SimpleNamespace(patcher=Patcher(named(types.SimpleNamespace(), {"qwen": BaseQwen3(**kw)})))
+    int8_gemv.patch(clip)
+    assert set(clip.patcher.patches) == {"qwen.logits", "qwen.generate"}
+    assert gemv_fakes.flash_attention_decode == "kitchen-original"
+
+
+def test_int8_gemv_patch_logits_needs_bf16_table(gemv_fakes):
+    clip = types.SimpleNamespace(patcher=Patcher(named(types.SimpleNamespace(), {"qwen": BaseQwen3(embed_dtype=torch.float16, fixed_kv=False)})))
+    int8_gemv.patch(clip)
+    assert set(clip.patcher.patches) == {"qwen.generate"}
+
+
+def test_generate_scopes_the_flag():
+    seen = []
+
+    class T:
+        def generate(self, *a, **k):
+            seen.append((int8_gemv.generating, a, k))
+            if k.get("fail"):
+                raise ValueError("stop")
+            return "tokens"
+
+    assert int8_gemv.generate(T(), 1, max_new=2) == "tokens"
+    with pytest.raises(ValueError):
+        int8_gemv.generate(T(), fail=True)
+    assert seen[0] == (True, (1,), {"max_new": 2}) and seen[1][0] is True and int8_gemv.generating is False
+
+
+class QTensor:
+    """A quantized weight whose dequantize() gives W * scale, as comfy's int8 QuantizedTensor does."""
+
+    def __init__(self, w, scale):
+        self.w, self.scale = w, scale
+
+    def to(self, dtype=None):
+        return QTensor(self.w, self.scale) if dtype is None else types.SimpleNamespace(dequantize=lambda: self.w.to(dtype) * self.scale.to(dtype)[:, None])
+
+
+def cast_context(monkeypatch):
+    calls = []
+
+    class CastBiasWeightContext:
+        def __init__(self, module, **kw):
+            self.module, self.kw = module, kw
+            calls.append(kw)
+
+        def __enter__(self):
+            return self.module.qweight, getattr(self.module, "bias", None)
+
+        def __exit__(self, *a):
+            return False
+
+    monkeypatch.setattr(int8_gemv, "comfy", types.SimpleNamespace(ops=types.SimpleNamespace(CastBiasWeightContext=CastBiasWeightContext)))
+    return calls
+
+
+def test_mlp_forward_merges_gate_and_up(monkeypatch):
+    calls = cast_context(monkeypatch)
+    g = torch.Generator().manual_seed(5)
+    K, N = 64, 96
+    wg, wu = (torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8) for _ in range(2))
+    sg, su = (torch.rand(N, generator=g) * 1e-2 for _ in range(2))
+
+    class Module:
+        def __init__(self):
+            self.gate_proj = types.SimpleNamespace(qweight=QTensor(wg, sg), weight_function=None, bias_function=None)
+            self.up_proj = types.SimpleNamespace(qweight=QTensor(wu, su), weight_function=None, bias_function=None)
+            self.activation = F.silu
+            self.down_proj = lambda h: h * 2
+
+        def forward(self, x, norm=None):
+            return "original"
+
+    m = Module()
+    x = torch.randn(3, K, generator=g)
+    monkeypatch.setattr(int8_gemv, "generating", True)
+    out = int8_gemv.mlp_forward(m, torch.int8, x)
+    ref = 2 * F.silu(x @ (wg.float() * sg[:, None]).T) * (x @ (wu.float() * su[:, None]).T)
+    assert torch.allclose(out, ref, rtol=1e-5, atol=1e-5)
+    assert len(calls) == 2 and all(c["want_requant"] and c["dtype"] is torch.int8 for c in calls)
+    # Fallbacks: outside generate(), a norm argument, fp16 x, one token, patched layers.
+    monkeypatch.setattr(int8_gemv, "generating", False)
+    assert int8_gemv.mlp_forward(m, torch.int8, x) == "original"
+    monkeypatch.setattr(int8_gemv, "generating", True)
+    assert int8_gemv.mlp_forward(m, torch.int8, x, norm="n") == "original"
+    assert int8_gemv.mlp_forward(m, torch.int8, x.half()) == "original"
+    assert int8_gemv.mlp_forward(m, torch.int8, x[:1]) == "original"
+    m.up_proj.weight_function = ["lora"]
+    assert int8_gemv.mlp_forward(m, torch.int8, x) == "original"
+
+
+def test_logits_fallbacks(monkeypatch):
+    class T:
+        def __init__(self, dtype=torch.bfloat16):
+            self.model = types.SimpleNamespace(embed_tokens=types.SimpleNamespace(weight_function=None))
+
+        def logits(self, x):
+            return "original"
+
+    t = T()
+    assert int8_gemv.logits(t, torch.zeros(2, 3, 8)) == "original"  # batch of 2
+    assert int8_gemv.logits(t, torch.zeros(1, 3, 8, dtype=torch.float16)) == "original"
+    t.model.embed_tokens.weight_function = ["patch"]
+    assert int8_gemv.logits(t, torch.zeros(1, 3, 8)) == "original"
+
+
+def test_linear_forward_prefill_uses_dequantized_matmul_only_inside_generate(monkeypatch):
+    """Several tokens with a ConvRot group above 256: the dequantized matmul inside generate(), the layer's own forward
+    outside it (int8_gemv.py:48-64); the rotation is a GPU kernel, so without a GPU the eligible call raises."""
+    class Lin:
+        weight_function = bias_function = None
+
+        @staticmethod
+        def forward(module, x, *a, **k):
+            return "original"
+
+    m = Lin()
+    m.__class__ = type("Linear", (Lin,), {})
+    x = torch.zeros(3, 1024)
+    assert int8_gemv.linear_forward(m, 64, 1024, torch.int8, 1024, x) == "original"  # outside generate()
+    monkeypatch.setattr(int8_gemv, "generating", True)
+    assert int8_gemv.linear_forward(m, 64, 1024, torch.int8, 256, x) == "original"  # group <= 256: kitchen's fast dequantize
+    if torch.cuda.is_available():
+        return
+    cast_context(monkeypatch)
+    m.qweight = types.SimpleNamespace(_qdata=torch.zeros(64, 1024, dtype=torch.int8), _params=types.SimpleNamespace(scale=torch.ones(64)))
+    monkeypatch.setattr(int8_gemv, "kernels", None)
+    monkeypatch.setattr(int8_gemv._lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        int8_gemv.linear_forward(m, 64, 1024, torch.int8, 1024, x)
+
+
+# ------------------------------------------------------------------------------------ rms_norm / int8_gemm patches
+
+def diffusion_model(tree):
+    dm = named(types.SimpleNamespace(), tree)
+    return Patcher(types.SimpleNamespace(diffusion_model=dm))
+
+
+def test_rms_norm_patch(monkeypatch):
+    class RMSNorm:
+        pass
+
+    monkeypatch.setattr(rms_norm, "RMSNorm", RMSNorm)
+    a, b = RMSNorm(), RMSNorm()
+    m = diffusion_model({"blocks.0.norm": a, "blocks.0.other": object(), "blocks.1.norm": b})
+    rms_norm.patch(m)
+    assert set(m.patches) == {"diffusion_model.blocks.0.norm.forward", "diffusion_model.blocks.1.norm.forward"}
+    p = m.patches["diffusion_model.blocks.1.norm.forward"]
+    assert p.func is rms_norm.forward and p.args == (b,)
+
+
+def test_patch_swiglu_and_patch_block(monkeypatch):
+    class SwiGLU:
+        pass
+
+    class SingleStreamBlock:
+        pass
+
+    monkeypatch.setattr(int8_gemm, "SwiGLU", SwiGLU)
+    monkeypatch.setattr(int8_gemm, "SingleStreamBlock", SingleStreamBlock)
+    s, blk = SwiGLU(), SingleStreamBlock()
+    m = diffusion_model({"b.0.mlp": s, "b.0": blk, "b.0.attn": object()})
+    int8_gemm.patch_swiglu(m)
+    assert set(m.patches) == {"diffusion_model.b.0.mlp.forward"}
+    assert m.patches["diffusion_model.b.0.mlp.forward"].func is int8_gemm.swiglu_forward
+    int8_gemm.patch_block(m, True)
+    p = m.patches["diffusion_model.b.0.forward"]
+    assert p.func is int8_gemm.block_forward and p.args == (blk, True)
+
+
+def test_swiglu_forward_routes(monkeypatch):
+    import fakes
+    fakes.install(monkeypatch)
+    int8_gemm.enable(True)
+    Layer = int8_gemm.originals["layer"]
+    seen = []
+
+    class Down(Layer):
+        def __call__(self, x):
+            seen.append((x, int8_gemm.swiglu_up))
+            return x
+
+    g = torch.Generator().manual_seed(3)
+    gate_x = torch.randn(4, 256, generator=g).half()
+    up_x = torch.randn(4, 256, generator=g).half()
+    module = types.SimpleNamespace(gate=lambda x: gate_x, up=lambda x: up_x, down=Down(256, 64))
+    # Fusable: down receives the raw gate, the up projection waits in the side channel.
+    int8_gemm.swiglu_forward(module, None)
+    assert seen[-1][0] is gate_x and seen[-1][1] is up_x
+    monkeypatch.setattr(int8_gemm, "swiglu_up", None)
+    # Not fusable (no Triton path, a LoRA'd down, or not an Int8 layer): silu(gate) * up in torch.
+    monkeypatch.setattr(int8_gemm, "swiglu_fusable", False)
+    int8_gemm.swiglu_forward(module, None)
+    assert torch.equal(seen[-1][0], F.silu(gate_x) * up_x) and seen[-1][1] is None
+    monkeypatch.setattr(int8_gemm, "swiglu_fusable", True)
+    module.down.lora_patches = ["lora"]
+    int8_gemm.swiglu_forward(module, None)
+    assert torch.equal(seen[-1][0], F.silu(gate_x) * up_x)
+    module.down = lambda x: ("plain", x)
+    assert int8_gemm.swiglu_forward(module, None)[0] == "plain"
+
+
+# ---------------------------------------------------------------------------------------------------- node shim
+
+def comfy_stubs():
+    """Stand-ins for the ComfyUI modules the node shim imports (comfy.patcher_extension, comfy.quant_ops,
+    comfy_api.latest)."""
+    comfy = types.ModuleType("comfy")
+    pe = types.ModuleType("comfy.patcher_extension")
+    pe.CallbacksMP = types.SimpleNamespace(ON_PRE_RUN="on_pre_run")
+    qo = types.ModuleType("comfy.quant_ops")
+
+    class QuantizedTensor(torch.Tensor):
+        pass
+
+    qo.QuantizedTensor = QuantizedTensor
+    api = types.ModuleType("comfy_api")
+    latest = types.ModuleType("comfy_api.latest")
+
+    def field(kind):
+        return types.SimpleNamespace(Input=lambda *a, **k: (kind, a, k), Output=lambda *a, **k: (kind, a, k))
+
+    latest.io = types.SimpleNamespace(ComfyNode=object, Schema=lambda **k: k, NodeOutput=lambda *a: a, Model=field("model"),
+                                      Combo=field("combo"), Boolean=field("bool"), Clip=field("clip"))
+    latest.ComfyExtension = object
+    comfy.patcher_extension, comfy.quant_ops = pe, qo
+    return {"comfy": comfy, "comfy.patcher_extension": pe, "comfy.quant_ops": qo, "comfy_api": api, "comfy_api.latest": latest}
+
+
+@pytest.fixture
+def shim(monkeypatch):
+    """The package loaded afresh, under its own name, with the ComfyUI stand-ins importable: the node classes exist."""
+    for name, mod in comfy_stubs().items():
+        monkeypatch.setitem(sys.modules, name, mod)
+    name = "rda_node_shim"
+    spec = importlib.util.spec_from_file_location(name, __graft_entry__.PKG_DIR + "/__init__.py", submodule_search_locations=[__graft_entry__.PKG_DIR])
+    pkg = importlib.util.module_from_spec(spec)
+    monkeypatch.setitem(sys.modules, name, pkg)
+    spec.loader.exec_module(pkg)
+    yield pkg
+    for key in [k for k in sys.modules if k.startswith(name + ".")]:
+        del sys.modules[key]
+
+
+class Model:
+    def __init__(self, dynamic=False, tree=None):
+        self.dynamic, self.calls, self.patches, self.callbacks = dynamic, [], {}, []
+        self.model = types.SimpleNamespace(diffusion_model=named(types.SimpleNamespace(), tree or {}))
+
+    def clone(self):
+        self.calls.append("clone")
+        return self
+
+    def set_model_optimized_attention(self, fn):
+        self.calls.append(("attention", fn))
+
+    def add_object_patch(self, name, obj):
+        self.patches[name] = obj
+
+    def get_model_object(self, name):
+        return getattr(self.model, name)
+
+    def is_dynamic(self):
+        return self.dynamic
+
+    def add_callback(self, kind, fn):
+        self.callbacks.append((kind, fn))
+
+
+def test_node_schemas(shim):
+    s = shim.RDNA2Attention.define_schema()
+    assert s["node_id"] == "RDNA2Attention"
+    names = [i[1][0] for i in s["inputs"]]
+    assert names == ["model", "backend", "transpose_weights", "int8_gemm", "fused_norm", "fused_swiglu"]
+    assert s["inputs"][1][2]["options"] == ["hip", "hip_int8", "bmm"] and s["inputs"][1][2]["default"] == "hip"
+    assert shim.RDNA2TextGenerate.define_schema()["node_id"] == "RDNA2TextGenerate"
+    import asyncio
+    ext = asyncio.run(shim.comfy_entrypoint())
+    assert asyncio.run(ext.get_node_list()) == [shim.RDNA2Attention, shim.RDNA2TextGenerate]
+
+
+def test_execute_call_sequence(shim, monkeypatch, caplog):
+    events = []
+    monkeypatch.setattr(shim.int8_kernels, "enable", lambda on: events.append(("enable", on)))
+    monkeypatch.setattr(shim.rms_norm, "patch", lambda m: events.append("rms_norm.patch"))
+    monkeypatch.setattr(shim.int8_kernels, "patch_swiglu", lambda m: events.append("patch_swiglu"))
+    monkeypatch.setattr(shim.int8_kernels, "patch_block", lambda m, q: events.append(("patch_block", q)))
+    m = Model()
+    out = shim.RDNA2Attention.execute(m, "hip")
+    assert out == (m,) and m.calls == ["clone", ("attention", shim.attention_hip)] and events == [("enable", False)]
+    events.clear()
+    shim.RDNA2Attention.execute(Model(), "hip_int8", int8_gemm=True, fused_norm=True, fused_swiglu=True)
+    assert events == [("enable", True), "rms_norm.patch", "patch_swiglu", ("patch_block", True)]
+    events.clear()
+    m = Model()
+    shim.RDNA2Attention.execute(m, "bmm", fused_norm=True, fused_swiglu=True)  # no fused block without a hip backend
+    assert events == [("enable", False), "rms_norm.patch", "patch_swiglu"] and m.calls[1] == ("attention", shim.attention_bmm)
+    m = Model()
+    shim.RDNA2Attention.execute(m, "hip", transpose_weights=True)
+    assert m.callbacks == [("on_pre_run", shim.relayout_weights)]
+    m = Model(dynamic=True)
+    with caplog.at_level(logging.WARNING):
+        shim.RDNA2Attention.execute(m, "hip", transpose_weights=True)
+    assert m.callbacks == [] and "transpose_weights skipped" in caplog.text
+
+
+def test_text_generate_execute(shim, monkeypatch):
+    seen = []
+    monkeypatch.setattr(shim.int8_gemv, "patch", lambda clip: seen.append(clip))
+    clip = Model()
+    assert shim.RDNA2TextGenerate.execute(clip) == (clip,) and seen == [clip] and clip.calls == ["clone"]
+
+
+def test_relayout_weights(shim):
+    """fp16 Linear weights of at least 1024 x 1024 off the CPU become K-major (same shape and values); CPU, small,
+    quantized, non-fp16 and already K-major weights are left alone. The meta device stands in for the GPU."""
+    big = torch.nn.Linear(1024, 2048, bias=False, device="meta", dtype=torch.float16)
+    small = torch.nn.Linear(512, 2048, bias=False, device="meta", dtype=torch.float16)
+    fp32 = torch.nn.Linear(1024, 1024, bias=False, device="meta")
+    cpu = torch.nn.Linear(1024, 1024, bias=False, dtype=torch.float16)
+    tree = types.SimpleNamespace(modules=lambda: [big, small, fp32, cpu, torch.nn.ReLU()])
+    patcher = types.SimpleNamespace(model=types.SimpleNamespace(diffusion_model=tree))
+    strides = [m.weight.stride() for m in (small, fp32, cpu)]
+    shim.relayout_weights(patcher)
+    assert big.weight.shape == (2048, 1024) and big.weight.stride() == (1, 2048)
+    assert [m.weight.stride() for m in (small, fp32, cpu)] == strides
+    shim.relayout_weights(patcher)  # already K-major: unchanged
+    assert big.weight.stride() == (1, 2048)
+
+
+def test_package_without_comfyui_defines_no_nodes():
+    pkg = sys.modules[__graft_entry__.PKG_NAME]
+    assert pkg.io is None and not hasattr(pkg, "RDNA2Attention")
