@@ -364,3 +364,45 @@ int rda_attn_merge(const float* partial, const float* stats, float* out, int hea
 int rda_decode_splits(void) { return SPLITS; }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- decode attention without allocation
+// For callers that cannot allocate device memory (code under HIP graph capture, tight serving loops): the split
+// partials and statistics of rda_attn_decode live in `scratch`, a file-scope device array sized for
+// NOALLOC_MAX_HEADS query heads (256 x 32 splits x (128 + 2) floats = 4.06 MiB), which every GPU the library runs
+// on holds until the process ends. In host code `scratch` only names the symbol: its device address on the current
+// GPU comes from hipGetSymbolAddress, once per device, and only that address is passed to the kernels. attn_decode
+// writes every (head, split) slot of the partials and statistics it reads back, so nothing needs clearing between
+// calls; calls that overlap on one GPU share the array and race.
+#define NOALLOC_MAX_HEADS 256
+static __device__ __align__(256) float scratch[NOALLOC_MAX_HEADS * SPLITS * (HEAD + 2)];
+static std::atomic<float*> scratch_on[RDA_MAX_DEVICES];
+
+// The device address of `scratch` on the current GPU (looked up on the first call for that GPU).
+static int scratch_address(float** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= RDA_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    float* p = scratch_on[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* addr = nullptr;
+        e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (addr == nullptr) return (int)hipErrorInvalidSymbol;
+        p = (float*)addr;
+        scratch_on[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return 0;
+}
+
+extern "C" int rda_attention_decode_noalloc(const float* q, const float* k, const float* v, const int* lengths, float* out, int B, int H, int Hkv,
+                                            int capacity, float scale, void* stream) {
+    if (B <= 0 || H <= 0 || (long)B * H > NOALLOC_MAX_HEADS) return RDA_ERR_INVALID;
+    float* base = nullptr;
+    if (const int e = scratch_address(&base)) return e;
+    float* partial = base;                                              // (B H, SPLITS, HEAD)
+    float* stats = base + (size_t)NOALLOC_MAX_HEADS * SPLITS * HEAD;    // (B H, SPLITS, 2)
+    if (const int e = rda_attn_decode(q, k, v, lengths, partial, stats, B, H, Hkv, capacity, scale, stream)) return e;
+    return rda_attn_merge(partial, stats, out, B * H, stream);
+}

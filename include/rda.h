@@ -124,6 +124,15 @@ int rda_attn_merge(const float* partial, const float* stats, float* out, int hea
 
 int rda_decode_splits(void);
 
+/* attention_decode without allocation. No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The same result as
+ * rda_attn_decode + rda_attn_merge, bit for bit; out (B, 1, H, 128) fp32. The split partials live in a device
+ * array inside the library (4.06 MiB per GPU, held until the process ends), so B * H must be <= 256: larger
+ * calls return 1 (hipErrorInvalidValue) without launching. Calls that overlap on one GPU share that array and
+ * race; serialise them (one stream, or events). Nothing is allocated, freed or cleared. */
+int rda_attention_decode_noalloc(const float* q, const float* k, const float* v, const int* lengths, float* out, int B, int H, int Hkv,
+                                 int capacity, float scale, void* stream);
+
 /* ------------------------------------------------------------------ RMSNorm -------------- */
 /* x (B, H, L, D) fp16 addressed by element strides sb, sh, sl (last dim contiguous); w fp32 [D],
  * zero-centred (the kernels use w + 1); y contiguous (B, H, L, D). */
