@@ -22,8 +22,10 @@ with the host's CPU model, logical CPU count and torch thread count under "host"
 "decode_layer" times one token through one Qwen3-8B-shaped layer's int8 linears and decode attention, and
 "dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192, 4096 tokens).
 
-`--only NAME` runs one workload (the names of "components", "attention_f16", or "copy": a 1 GiB device copy used to
-calibrate FETCH_SIZE / WRITE_SIZE) and prints its line; the rocprofv3 summaries in profiles/ are made that way.
+`--only NAME` runs one workload (the names of "components", "attention_f16", "copy": a 1 GiB device copy used to
+calibrate FETCH_SIZE / WRITE_SIZE, or "mfma_peak_i8" / "mfma_peak_f16": back-to-back MFMAs, the sustained matrix rate)
+and prints its line; the rocprofv3 summaries in profiles/ are made that way. The default run also reports the
+measured MFMA peaks and the shader clock they ran at under "calibration".
 """
 import argparse
 import json
@@ -274,42 +276,63 @@ def w_decode_attention(torch, dev):
 def w_decode_layer(torch, dev):
     """One token through one Qwen3-8B-shaped layer as int8_gemv's patched forwards run it (int8_gemv.py:48-64,
     111-113): hidden 4096, 32 query / 8 KV heads of 128, MLP 12288, KV cache length 2048 (fp32). Each of the seven
-    int8 linears is linear_forward's single-token path -- ConvRot of its fp32 input (group 256, int8_gemv.rotate)
-    then the GEMV (int8_gemv.gemv) -- and attention is int8_gemv.attention_decode; the layer's own torch ops (norms,
-    rope, silu * up, residual adds) are outside this path and not included. Replayed from a HIP graph, as a decode
-    loop would, over enough weight and cache copies that the Infinity Cache cannot serve them. Bytes: the int8
-    weights, their scales, the K/V cache and the activations read and written."""
+    int8 linears is int8_gemv.linear_forward's single-token path -- the ConvRot of its fp32 input (group 256; q, k
+    and v read one input, as do gate and up, so one rotation serves each group of them) then the GEMV -- with a
+    stand-in for ComfyUI's quantized-weight context handing it the layer's int8 weight; attention is
+    int8_gemv.attention_decode; the layer's own torch ops (norms, rope, silu * up, residual adds) are outside this
+    path and not included. Replayed from a HIP graph, as a decode loop would, over enough weight and cache copies
+    that the Infinity Cache cannot serve them. Bytes: the int8 weights, their scales, the K/V cache and the
+    activations read and written."""
+    import types
     from comfyui_rdna2_attention_amd import int8_gemv
     D, Hq, Hkv, F, cap = 4096, 32, 8, 12288, 2048
     shapes = {"q": (D, D), "k": (Hkv * 128, D), "v": (Hkv * 128, D), "o": (D, D), "gate": (F, D), "up": (F, D), "down": (D, F)}
     weights_bytes = sum(n * k for n, k in shapes.values())
     kv_bytes = 2 * cap * Hkv * 128 * 4
     copies = max(1, ROTATE_BYTES // (weights_bytes + kv_bytes) + 1)
+    pairs = {}
+
+    class CastBiasWeightContext:  # comfy.ops' context: yields the module's (weight, bias)
+        def __init__(self, module, **kwargs):
+            self.pair = pairs[id(module)]
+
+        def __enter__(self):
+            return self.pair
+
+        def __exit__(self, *exc):
+            return False
+
+    int8_gemv.comfy = types.SimpleNamespace(ops=types.SimpleNamespace(CastBiasWeightContext=CastBiasWeightContext))
     g = gen(torch, 40)
     layers = []
     for _ in range(copies):
-        w = {name: torch.randint(-127, 128, shp, generator=g, dtype=torch.int8).to(dev) for name, shp in shapes.items()}
-        s = {name: (torch.rand(shp[0], generator=g) * 2e-3 + 1e-3).float().to(dev) for name, shp in shapes.items()}
+        mods = {}
+        for name, (n, k) in shapes.items():
+            mods[name] = types.SimpleNamespace(weight_function=[], bias_function=[])
+            w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
+            s = (torch.rand(n, generator=g) * 2e-3 + 1e-3).float().to(dev)
+            pairs[id(mods[name])] = (types.SimpleNamespace(_qdata=w, _params=types.SimpleNamespace(scale=s)), None)
         kv = [torch.randn(1, cap, Hkv, 128, generator=g).float().to(dev) for _ in range(2)]
-        layers.append((w, s, kv))
+        layers.append((mods, kv))
     x = torch.randn(1, 1, D, generator=g).float().to(dev)
     lengths = torch.full((1,), cap, dtype=torch.int32, device=dev)
 
-    def lin(name, w, s, inp):
-        return int8_gemv.gemv(int8_gemv.rotate(inp, 256), w[name], s[name])
+    def lin(mods, name, inp):
+        n, k = shapes[name]
+        return int8_gemv.linear_forward(mods[name], n, k, torch.int8, 256, inp)
 
     def step(i):
-        w, s, (kc, vc) = layers[i]
-        q = lin("q", w, s, x)
-        lin("k", w, s, x)
-        lin("v", w, s, x)
+        mods, (kc, vc) = layers[i]
+        q = lin(mods, "q", x)
+        lin(mods, "k", x)
+        lin(mods, "v", x)
         o = int8_gemv.attention_decode(q.view(1, 1, Hq, 128), kc, vc, lengths)
-        h = lin("o", w, s, o.view(1, 1, D))
-        gate = lin("gate", w, s, h)
-        lin("up", w, s, h)
-        return lin("down", w, s, gate)
+        h = lin(mods, "o", o.view(1, 1, D))
+        gate = lin(mods, "gate", h)
+        lin(mods, "up", h)
+        return lin(mods, "down", gate)
 
-    act = 4 * (D * 10 + Hkv * 128 * 2 + F * 4)  # fp32 inputs read (7 rotations, 7 GEMVs) and outputs written, roughly
+    act = 4 * (D * 7 + Hkv * 128 * 2 + F * 4)  # fp32 inputs read (4 rotations, 7 GEMVs) and outputs written, roughly
     work = weights_bytes + 4 * sum(n for n, _ in shapes.values()) + kv_bytes + act
     return step, copies, work, "hbm", graph_timed
 
@@ -340,6 +363,37 @@ def w_dit_block(torch, dev):
     return (lambda i: int8_gemm.block_forward(blk, False, x, None, freqs)), 1, work, "mfma_i8", event_timed
 
 
+CALIB_BLOCKS, CALIB_ITERS = 2048, 2000
+
+
+def w_mfma_peak(torch, dev, int8):
+    """Back-to-back independent MFMAs on every SIMD (csrc/calib.hip): the matrix rate this GPU sustains."""
+    from comfyui_rdna2_attention_amd import _lib
+    out = torch.empty(CALIB_BLOCKS * 256, dtype=torch.int32, device=dev)
+    clocks = torch.zeros(2, dtype=torch.int64, device=dev)
+    lib = _lib.load()
+    fn = lambda i: _lib.check(lib.rda_calib_mfma_peak(int(int8), CALIB_BLOCKS, CALIB_ITERS, _lib.ptr(out), _lib.ptr(clocks), _lib.stream()))  # noqa: E731
+    fn.clocks = clocks
+    work = CALIB_BLOCKS * 4.0 * CALIB_ITERS * 8 * (65536 if int8 else 32768)
+    return fn, 1, work, "mfma_i8" if int8 else "mfma_f16", event_timed
+
+
+def calibrate(torch, dev, steps, warmup):
+    """Measured MFMA peaks (int8, fp16) and the shader clock they ran at (shader-clock ticks over 100 MHz real-time
+    ticks of one wave)."""
+    res = {}
+    for name, int8 in (("mfma_i8", True), ("mfma_f16", False)):
+        fn, _, work, bound, timer = w_mfma_peak(torch, dev, int8)
+        _, kms = timer(torch, fn, steps, warmup)
+        ticks, rt = (int(v) for v in fn.clocks.cpu())
+        peak = PEAKS[bound][1]
+        rate = work / kms / 1e9
+        res[name] = {"value": round(rate, 1), "unit": "TOP/s" if int8 else "TFLOP/s", "frac_of_nominal": round(rate / peak, 4),
+                     "shader_clock_ghz": round(ticks / (rt / 100e6) / 1e9, 3) if rt > 0 else None}
+        log(f"calibration {name}: {rate:.1f} ({rate / peak * 100:.1f}% of nominal), shader clock {res[name]['shader_clock_ghz']} GHz")
+    return res
+
+
 def w_copy(torch, dev):
     """An elementwise kernel that reads 1 GiB and writes 1 GiB (torch.neg on fp32): the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters."""
@@ -365,13 +419,16 @@ WORKLOADS = {
     "decode_layer": w_decode_layer,
     "dit_block": w_dit_block,  # last: it installs the hooks over stand-in plugin modules for the rest of the run
     "copy": w_copy,
+    "mfma_peak_i8": lambda t, d: w_mfma_peak(t, d, True),
+    "mfma_peak_f16": lambda t, d: w_mfma_peak(t, d, False),
 }
+NOT_COMPONENTS = ("attention_f16", "copy", "mfma_peak_i8", "mfma_peak_f16")
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}
 # The roofline of each workload (the 4th item its function returns), for the CPU leg, which runs without a GPU.
 WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
                   "w4a8_gemm": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
                   "decode_gemv_n1024": "hbm", "decode_gemv_n12288": "hbm", "decode_attention": "hbm", "decode_layer": "hbm", "dit_block": "mfma_i8",
-                  "copy": "hbm"}
+                  "copy": "hbm", "mfma_peak_i8": "mfma_i8", "mfma_peak_f16": "mfma_f16"}
 
 
 def run_workload(torch, dev, name, steps, warmup, traffic):
@@ -497,7 +554,7 @@ def c_decode_layer(torch):
     kc, vc = (torch.randn(1, cap, Hkv, 128, generator=g) for _ in range(2))
     x = torch.randn(1, 1, D, generator=g)
     H = cb.hadamard(256)
-    work = sum(n * k for n, k in shapes.values()) + 4 * sum(n for n, _ in shapes.values()) + 2 * cap * Hkv * 512 + 4 * (D * 10 + Hkv * 256 + F * 4)
+    work = sum(n * k for n, k in shapes.values()) + 4 * sum(n for n, _ in shapes.values()) + 2 * cap * Hkv * 512 + 4 * (D * 7 + Hkv * 256 + F * 4)
     return (lambda: cb.decode_layer(x, w, s, kc, vc, cap, Hq, 256, H)), work, \
         "seven ConvRot + dequantized single-token linears and fp32 decode attention of one Qwen3-8B-shaped layer"
 
@@ -610,7 +667,8 @@ def main():
     }
     if not args.no_components:
         result["components"] = {name: run_workload(torch, dev, name, args.steps, args.warmup, traffic)
-                                for name in WORKLOADS if name not in ("attention_f16", "copy")}
+                                for name in WORKLOADS if name not in NOT_COMPONENTS}
+        result["calibration"] = calibrate(torch, dev, args.steps, args.warmup)
     if not args.no_cpu:
         # The headline's sample is larger (6 of 24 heads, about 10 s); each component's is about 1.5 s.
         result["cpu_baseline"] = cpu_baseline(torch, "attention_f16", seconds=10.0, heads=6)

@@ -59,6 +59,38 @@ def rotate(x, group):
     return rotated
 
 
+# The ConvRot of the last single-token input. Consecutive linears that read the same activation -- q, k and v of an
+# attention layer, gate and up of an MLP -- rotate it once. An entry is reused only for the same tensor object (held
+# here, so its memory cannot be handed to another tensor meanwhile), at the same version counter (in-place writes
+# bump it; inference tensors have none, and are matched by object alone), the same group, and the same graph-capture
+# state (a rotation launched outside a capture is never read inside one, nor the reverse).
+_last_rotation = None
+
+
+def _version(x):
+    try:
+        return x._version
+    except RuntimeError:  # inference tensors do not track versions
+        return None
+
+
+def rotate_once(x, group):
+    """rotate(x, group), or the rotation of the previous call when it had this same input."""
+    global _last_rotation
+    capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
+    hit = _last_rotation
+    if hit is not None and hit[0] is x and hit[1] == _version(x) and hit[2] == group and hit[3] == capturing:
+        return hit[4]
+    rotated = rotate(x, group)
+    _last_rotation = (x, _version(x), group, capturing, rotated)
+    return rotated
+
+
+def forget_rotation():
+    global _last_rotation
+    _last_rotation = None
+
+
 def gemv(x, weight, scale, bias=None):
     """out[n] = scale[n] * dot(weight[n], x) (+ bias[n]) for one row x (K values, fp32 or fp16; the output has its dtype),
     weight (N, K) int8, scale (N,) fp32, bias (N,) fp32 or None."""
@@ -78,7 +110,7 @@ def linear_forward(module, N, K, weight_dtype, group, x, *args, **kwargs):
     x = x.contiguous()
     with quantized_weight(module, weight_dtype, x) as (weight, bias):
         if group:
-            x = rotate(x, group)
+            x = rotate_once(x, group)
         scale = weight._params.scale.to(device=x.device)
         if not single:
             return F.linear(x, weight._qdata.to(x.dtype) * scale, bias)
@@ -98,10 +130,12 @@ def mlp_forward(module, weight_dtype, x, norm=None):
 def generate(transformer, *args, **kwargs):
     global generating
     generating = True
+    forget_rotation()
     try:
         return type(transformer).generate(transformer, *args, **kwargs)
     finally:
         generating = False
+        forget_rotation()
 
 
 def logits_gemv(x, weight):

@@ -148,6 +148,13 @@ int rda_rms_norm_row(const void* x, const float* w, void* y, int B, int H, int L
 int rda_rms_norm_rope(const void* x, const float* w, void* y, int B, int H, int L, int D, long sb, long sh, long sl, float eps, const float* freqs,
                       long fb, void* stream);
 
+/* ------------------------------------------------------------------ calibration -------- */
+/* Measurement only, no counterpart in the reference: `blocks` workgroups of four waves each issue `iters` rounds of
+ * 8 independent MFMAs (int8 = 1: v_mfma_i32_32x32x32_i8, 65536 ops each; int8 = 0: v_mfma_f32_32x32x16_f16, 32768
+ * FLOP each), back to back. out: blocks * 256 ints (written to keep the products live); clocks[0] = shader-clock
+ * ticks and clocks[1] = 100 MHz real-time ticks over the run of workgroup 0's first wave. */
+int rda_calib_mfma_peak(int int8, int blocks, int iters, int* out, long long* clocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,7 +37,10 @@ def gemv_bound(w, x, scale, half):
 
 
 @pytest.mark.parametrize("x_half", [False, True])
-@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536)])
+# one row per wave: (4096, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536), (1000, 1536); K split over 4 waves per
+# row: (1024, 4096), (1002, 16384), (8, 4096); over 2: (2048, 8192), (1500, 2048)
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536), (1000, 1536), (1002, 16384),
+                                 (8, 1024), (2048, 8192), (1500, 2048)])
 def test_gemv_i8(dev, N, K, x_half):
     print(f"gemv_i8 N={N} K={K} half={x_half}", flush=True)
     x = torch.randn(1, K, generator=gen(16))

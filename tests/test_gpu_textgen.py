@@ -61,6 +61,39 @@ def test_linear_forward_single_token(dev, monkeypatch, N, K, bias, group):
     assert np.all(err <= bound), f"max err {err.max():.3e}"
 
 
+def test_linear_forward_shares_one_rotation(dev, monkeypatch):
+    """q, k and v read one input: the first linear rotates it and the next two reuse that rotation (int8_gemv's
+    rotate_once); each output matches the oracle, and after an in-place write to the input the next call rotates
+    the new values."""
+    K = 4096
+    layers, pairs, refs = [], {}, []
+    for i, N in enumerate((4096, 1024, 1024)):
+        w, s = int8_weights(N, K, seed=40 + i), channel_scales(N, seed=50 + i)
+        layer = int8_layer()
+        pairs[id(layer)] = (types.SimpleNamespace(_qdata=w.to(dev), _params=types.SimpleNamespace(scale=s.to(dev))), None)
+        layers.append((layer, N, w, s))
+    stand_in_comfy(monkeypatch, pairs)
+    int8_gemv.forget_rotation()
+    x = torch.randn(1, 1, K, generator=gen(60)).float().to(dev)
+
+    def check(layer, N, w, s, out):
+        xr = oracle.rotate_f32(x.cpu().numpy().reshape(1, K), 256).reshape(-1)
+        ref = oracle.gemv_f64(xr, w.numpy(), s.numpy())
+        bound = 1e-5 * (np.abs(w.numpy().astype(np.float64)) @ np.abs(xr.astype(np.float64))) * np.abs(s.numpy()) + 1e-12
+        assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - ref) <= bound)
+
+    outs = [int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x) for layer, N, _, _ in layers]
+    rotated = int8_gemv._last_rotation[4]
+    for (layer, N, w, s), out in zip(layers, outs):
+        check(layer, N, w, s, out)
+    x.mul_(-0.5)
+    layer, N, w, s = layers[0]
+    out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+    assert int8_gemv._last_rotation[4] is not rotated
+    check(layer, N, w, s, out)
+    int8_gemv.forget_rotation()
+
+
 def test_logits_of_the_last_position(dev, monkeypatch):
     N, K, L = 4096, 2560, 7
     table = torch.randn(N, K, generator=gen(34)).bfloat16()

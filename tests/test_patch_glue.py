@@ -435,3 +435,34 @@ def test_relayout_weights(shim):
 def test_package_without_comfyui_defines_no_nodes():
     pkg = sys.modules[__graft_entry__.PKG_NAME]
     assert pkg.io is None and not hasattr(pkg, "RDNA2Attention")
+
+
+def test_rotation_reused_by_consecutive_linears(monkeypatch):
+    """rotate_once: one rotation for consecutive linears on the same input (q/k/v, gate/up); a new one for another
+    object, another group, after an in-place write, and after generate() starts or ends."""
+    calls = []
+    monkeypatch.setattr(int8_gemv, "rotate", lambda x, group: calls.append(group) or x * 2)
+    int8_gemv.forget_rotation()
+    x = torch.randn(1, 512)
+    a = int8_gemv.rotate_once(x, 256)
+    assert int8_gemv.rotate_once(x, 256) is a and int8_gemv.rotate_once(x, 256) is a and len(calls) == 1
+    int8_gemv.rotate_once(x, 64)
+    assert len(calls) == 2
+    b = int8_gemv.rotate_once(x, 64)
+    x.add_(1)  # an in-place write bumps the version counter
+    c = int8_gemv.rotate_once(x, 64)
+    assert c is not b and len(calls) == 3 and torch.equal(c, x * 2)
+    int8_gemv.rotate_once(x.clone(), 64)
+    assert len(calls) == 4
+    with torch.inference_mode():
+        z = torch.randn(1, 512)
+        assert int8_gemv.rotate_once(z, 256) is int8_gemv.rotate_once(z, 256) and len(calls) == 5
+
+    class T:
+        def generate(self):
+            return "tokens"
+
+    int8_gemv.rotate_once(x, 64)
+    int8_gemv.generate(T())
+    int8_gemv.rotate_once(x, 64)
+    assert len(calls) == 7
