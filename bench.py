@@ -211,6 +211,21 @@ def w_w4a8_gemm(torch, dev):
     return fn, 1, 2.0 * M * N * K, "mfma_i8", event_timed
 
 
+def w_w4a8_gemm_k12288(torch, dev):
+    """W4A8 at the down projection of the same MLP: M=4096, K=12288, N=3072 (group-128 fp16 scales) -- past K = 3456,
+    where the block's group scales take one block per CU."""
+    from comfyui_rdna2_attention_amd import _lib, int8_gemm
+    M, K, N = 4096, 12288, 3072
+    k, p = int8_gemm.get_kernels(), _lib.ptr
+    x = torch.randn(M, K, generator=gen(torch, 23)).half().to(dev)
+    w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 24), dtype=torch.uint8).to(dev)
+    gs = (torch.rand(N, K // 128, generator=gen(torch, 25)) * 1.5e-2 + 5e-3).half().to(dev)
+    a, s = int8_gemm.quantize(k.rot_quant_pack_a, x, K)
+    c = torch.empty(M, N, dtype=torch.float16, device=dev)
+    fn = lambda i: _lib.check(k.gemm_w4a8(p(a), p(w4), p(s), p(gs), None, p(c), M, N, K, 128, _lib.stream()))  # noqa: E731
+    return fn, 1, 2.0 * M * N * K, "mfma_i8", event_timed
+
+
 def w_mlp_rms_norm(torch, dev):
     from comfyui_rdna2_attention_amd import rms_norm
     M, K = 4096, 3072
@@ -409,6 +424,7 @@ WORKLOADS = {
     "w8a8_rot_quant": w_w8a8_rot_quant,
     "w8a8_linear": w_w8a8_linear,
     "w4a8_gemm": w_w4a8_gemm,
+    "w4a8_gemm_k12288": w_w4a8_gemm_k12288,
     "mlp_rms_norm": w_mlp_rms_norm,
     "mlp_swiglu_rot_quant": w_mlp_swiglu_rot_quant,
     "mlp_down_gemm": w_mlp_down_gemm,
@@ -426,7 +442,7 @@ NOT_COMPONENTS = ("attention_f16", "copy", "mfma_peak_i8", "mfma_peak_f16")
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}
 # The roofline of each workload (the 4th item its function returns), for the CPU leg, which runs without a GPU.
 WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
-                  "w4a8_gemm": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
+                  "w4a8_gemm": "mfma_i8", "w4a8_gemm_k12288": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
                   "decode_gemv_n1024": "hbm", "decode_gemv_n12288": "hbm", "decode_attention": "hbm", "decode_layer": "hbm", "dit_block": "mfma_i8",
                   "copy": "hbm", "mfma_peak_i8": "mfma_i8", "mfma_peak_f16": "mfma_f16"}
 
@@ -495,6 +511,17 @@ def c_w4a8_gemm(torch):
     xr = cb.rotate(x, 256)
     return (lambda: cb.linear_w4_dequant(xr, w4, gs)), 2.0 * M * N * K, \
         "int4 unpacked, group-128 scales applied, F.linear in fp32, the full 4096x12288x3072"
+
+
+def c_w4a8_gemm_k12288(torch):
+    from oracle import cpu_baseline as cb
+    M, K, N = 4096, 12288, 3072
+    x = torch.randn(M, K, generator=gen(torch, 23)).half().float()
+    w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 24), dtype=torch.uint8)
+    gs = (torch.rand(N, K // 128, generator=gen(torch, 25)) * 1.5e-2 + 5e-3).half()
+    xr = cb.rotate(x, 256)
+    return (lambda: cb.linear_w4_dequant(xr, w4, gs)), 2.0 * M * N * K, \
+        "int4 unpacked, group-128 scales applied, F.linear in fp32, the full 4096x3072x12288"
 
 
 def c_mlp_rms_norm(torch):
@@ -587,6 +614,7 @@ CPU_BASELINES = {
     "w8a8_rot_quant": c_w8a8_rot_quant,
     "w8a8_linear": c_w8a8_linear,
     "w4a8_gemm": c_w4a8_gemm,
+    "w4a8_gemm_k12288": c_w4a8_gemm_k12288,
     "mlp_rms_norm": c_mlp_rms_norm,
     "mlp_swiglu_rot_quant": c_mlp_swiglu_rot_quant,
     "mlp_down_gemm": c_mlp_down_gemm,

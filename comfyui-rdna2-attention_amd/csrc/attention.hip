@@ -66,9 +66,19 @@ struct Tile {
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
 
-// Transposing 8-byte LDS read (see the header).
-__device__ __forceinline__ h4v read_tr(const char* lds) {
-    return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)lds));
+// LDS reads by 32-bit LDS offset (no generic pointers in the tile loop, so a stage's constant offset folds into the
+// instruction's offset field): a 16-byte read, and the transposing 8-byte read (see the header).
+typedef __attribute__((address_space(3))) h8 lds_h8_t;
+__device__ __forceinline__ h8 lds_h8(u32 addr) { return *(const lds_h8_t*)(size_t)addr; }
+__device__ __forceinline__ h4v read_tr(u32 addr) {
+    return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)(size_t)addr));
+}
+// max(a, b, c) as one v_max3_f32. The scores come from MFMAs, which never produce signalling NaNs, so the quieting
+// the compiler would insert before fmaxf on values it cannot prove quiet is not needed.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float d;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
 }
 // (x of lanes 0-31, x of lanes 32-63) for every lane: the two halves of a query row.
 __device__ __forceinline__ f2 halves(float x) {
@@ -198,9 +208,10 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         ks_rd = (u32)(KB * 128 + 16 * g);
         asm volatile("" : "+v"(ks_rd));
     }
+    const u32 smem_u = lds_addr(smem);  // the dynamic LDS base, folded into the per-lane offsets below
     {
         const int sg = lane & 15;
-        const u32 vt = (u32)(T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
+        const u32 vt = smem_u + (u32)(T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
         const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) v_rd[dt] = vt + (u32)(((4 * dt) ^ vx) << 4);
@@ -211,24 +222,28 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 #pragma unroll
     for (int i = 0; i < 4; i++) asm volatile("" : "+v"(v_rd[i]));
 
+    // The fp16 K reads of a lane: row lq of the stage, chunk 2 ks + g at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx, i.e. byte
+    // offset ((kx << 4) ^ 32 ks) + 256 lq -- one xor-add per read from two values held for the whole loop.
+    u32 k_row = smem_u + (u32)(lq * 256), k_x16 = (u32)(((lane & 15) ^ g) << 4);
+    asm volatile("" : "+v"(k_row), "+v"(k_x16));
+
     // S^T of the tile in stage ST (scaled for int8), into s.
     float s[16];
     auto scores = [&](auto stage) __attribute__((always_inline)) {
         const char* st = smem + decltype(stage)::value * T::BYTES;
+        constexpr u32 st_u = decltype(stage)::value * T::BYTES;  // the stage: an immediate offset of the reads
         if (!I8) {
-            // K operands in two batches of four reads; each batch goes out before the products that use it.
-            // Their addresses are recomputed per tile from an opaque copy of the lane id: eight more VGPRs held
-            // across the loop would spill.
-            int ln = lane;
-            asm volatile("" : "+v"(ln));
-            const char* krow = st + (ln & 31) * 256;
-            const int kx = (ln & 15) ^ (ln >> 5);  // chunk 2 ks + g sits at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx
+            // K operands in two batches of four reads; each batch goes out before the products that use it. The row
+            // offset passes through an empty asm in every tile, so the eight addresses are made where they are read
+            // (one xor-add each) rather than hoisted out of the loop into eight more VGPRs.
+            u32 kr = k_row;
+            asm volatile("" : "+v"(kr));
             f16v acc = {};
 #pragma unroll
             for (int half_k = 0; half_k < 2; half_k++) {
                 h8 ka[4];
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++) ka[k4] = *(const h8*)(krow + (((2 * (half_k * 4 + k4)) ^ kx) << 4));
+                for (int k4 = 0; k4 < 4; k4++) ka[k4] = lds_h8(((k_x16 ^ (u32)(32 * (half_k * 4 + k4))) + kr) + st_u);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int k4 = 0; k4 < 4; k4++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4], qf[half_k * 4 + k4], acc, 0, 0, 0);
@@ -262,11 +277,12 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             for (int r = 0; r < 16; r++)
                 if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[r] = -1e30f;
         }
-        float mx = s[0];
+        float mx = max3(s[0], s[1], s[2]);
 #pragma unroll
-        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[r]);
+        for (int r = 3; r < 15; r += 2) mx = max3(mx, s[r], s[r + 1]);
+        mx = max3(mx, s[15], s[15]);
         const f2 mh = halves(mx);
-        mx = fmaxf(mh[0], mh[1]);
+        mx = max3(mh[0], mh[1], mh[1]);
         if (!I8) mx *= p.scale_log2;
         if (__any(mx > m + 8.f)) {
             const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
@@ -288,11 +304,11 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // O^T += V^T P^T with the V tile of stage ST and P in pf; the second step's V^T operands are read while the
     // first step's products run.
     auto pv = [&](auto stage) __attribute__((always_inline)) {
-        const char* st = smem + decltype(stage)::value * T::BYTES;
+        constexpr u32 st_u = decltype(stage)::value * T::BYTES;
         auto read_v = [&](h8 (&va)[4], int j) __attribute__((always_inline)) {
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) {
-                const char* ra = st + v_rd[dt] + 16 * j * 256;
+                const u32 ra = v_rd[dt] + st_u + 16 * j * 256;
                 va[dt] = __builtin_shufflevector(read_tr(ra), read_tr(ra + 8 * 256), 0, 1, 2, 3, 4, 5, 6, 7);
             }
         };

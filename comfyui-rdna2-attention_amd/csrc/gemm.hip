@@ -706,8 +706,12 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
         // One group per 128-wide slice. 128 x 128 blocks leave room for two blocks per CU, so one block's group
         // folds (vector ALU) overlap the other's products. Each wave takes all 128 rows and 32 columns: one int4
         // fragment to widen per k step instead of two (as 64 x 64), for two more A fragment reads from LDS.
+        // The block's group scales are staged whole (BN x K / 128 halves), so past K = 3456 two blocks no longer fit a
+        // CU's LDS: then one block per CU, which holds the scales of K up to ~45000.
         if (group != 128 || K % 128 != 0 || N % 128 != 0) return -1;
-        return launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        if (e >= 0) return e;
+        return launch_gemm8<128, 128, 128, 3, W4, EPI, 1, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
     } else {
         // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
         const bool wide = K % 128 == 0;
