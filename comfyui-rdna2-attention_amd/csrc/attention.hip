@@ -4,24 +4,30 @@
 //
 // Arithmetic follows attn / attn_i8 (hip_attention.hip:160-373): scores s in fp32; the running
 // maximum m only moves when some row's block maximum exceeds m + 8 (the lazy rescale,
-// hip_attention.hip:333-340); p = exp2(s * scale_log2 - m) (int8: exp2(s - m) with s already
-// scaled); P is rounded to fp16 before PV and l sums those fp16 values (in fp32, by v_dot2 with
-// ones, which halves the adds; the reference sums the fp32 p); out = fp16(o * (1 / l)).
+// hip_attention.hip:333-340; applied to the whole wave when any of its rows needs it); p =
+// exp2(s * scale_log2 - m) (int8: exp2(s - m) with s already scaled); P is rounded to fp16
+// before PV and l sums those fp16 values (in fp32, by v_dot2 with ones, which halves the adds;
+// the reference sums the fp32 p); out = fp16(o * (1 / l)). The block maximum is only computed
+// when a tile's P, made first with the current m, shows that a row may need the rescale (see
+// settle below): the outcome is the same as computing it for every tile.
 //
 // Work split. A workgroup of four wave64s owns 128 query rows of one (batch, head) and walks the
 // whole key range; each wave owns 32 query rows and keeps Q, O, l and m for them in registers
-// (<= 168 VGPRs). Three workgroups share a CU (three waves per SIMD, 2 x 16 KiB of LDS each), so
+// (<= 168 VGPRs). Three workgroups share a CU (three waves per SIMD, 3 x 16 KiB of LDS each), so
 // the attention configuration (24 heads x 4096 rows = 768 workgroups) runs in one round, and
 // while one workgroup waits at its barrier or for LDS, the others keep the matrix cores busy
 // (one eight-wave workgroup per CU, with two waves per SIMD in lockstep between barriers, left
 // the matrix cores idle for half the cycles). Block ids are remapped so that the workgroups an
 // XCD runs together belong to one head and share its K/V through that XCD's L2.
 //
-// Tiles. Each workgroup double-buffers 32-key tiles of K and V in LDS. They are copied by direct
-// global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes at LDS
-// base + 16 i), issued one whole tile ahead, so no register holds a tile in flight and the
-// load latency hides behind a full tile of work; the s_waitcnt before each tile's closing
-// barrier is where the next tile is awaited. Both tiles are row-major, 256 bytes per key
+// Tiles. Each workgroup keeps 32-key tiles of K and V in three LDS stages. They are copied by
+// direct global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes at LDS
+// base + 16 i), issued one step ahead, so no register holds a tile in flight and the load
+// latency hides behind a full step of work; the s_waitcnt before each step's closing barrier is
+// where the copies are awaited. The loop is software-pipelined: step i computes the scores of
+// tile i + 1 while tile i's exponentials run between those products (the transcendental unit
+// works beside the matrix cores; plain VALU work does not), then tile i's PV product -- so
+// tiles i and i + 1 are read while tile i + 2 arrives. Both tiles are row-major, 256 bytes per key
 // (int8 K: 128), with the 16-byte chunks of a row permuted by an XOR swizzle so that the
 // reads below hit distinct banks: K chunk c of key r sits at c ^ (r & 15) (int8: c ^ (r & 7)),
 // V chunk c at c ^ 4 (r & 3).
@@ -60,7 +66,7 @@ struct Tile {
     static constexpr int K_BYTES = KB * K_ROW + SC_BYTES;
     static constexpr int V_BYTES = KB * 256;
     static constexpr int BYTES = K_BYTES + V_BYTES;  // one stage: K, then V
-    static constexpr int LDS = 2 * BYTES;
+    static constexpr int LDS = 3 * BYTES;  // three stages
 };
 
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -73,18 +79,16 @@ __device__ __forceinline__ h8 lds_h8(u32 addr) { return *(const lds_h8_t*)(size_
 __device__ __forceinline__ h4v read_tr(u32 addr) {
     return __builtin_bit_cast(h4v, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4_t*)(size_t)addr));
 }
-// max(a, b, c) as one v_max3_f32. The scores come from MFMAs, which never produce signalling NaNs, so the quieting
-// the compiler would insert before fmaxf on values it cannot prove quiet is not needed.
-__device__ __forceinline__ float max3(float a, float b, float c) {
-    float d;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
-    return d;
-}
 // (x of lanes 0-31, x of lanes 32-63) for every lane: the two halves of a query row.
 __device__ __forceinline__ f2 halves(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return (f2){__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
+
+// The stage after `s` of the three: at compile time for a constant stage, at run time otherwise.
+template <int N>
+__device__ __forceinline__ constexpr std::integral_constant<int, (N + 1) % 3> next_stage(std::integral_constant<int, N>) { return {}; }
+__device__ __forceinline__ int next_stage(int s) { return s == 2 ? 0 : s + 1; }
 
 template <bool I8>
 __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_kernel(AttnArgs p) {
@@ -178,9 +182,9 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             dma16((const char*)k8base + (size_t)key0 * 128, k8_off, st + wq * 1024);
             if (wq == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, st + KB * 128);
         }
+        const char* kt = (const char*)kbase + key0 * skl2;
+        const char* vt = (const char*)vbase + key0 * svl2;
         if (key0 + KB <= p.Lk) {
-            const char* kt = (const char*)kbase + key0 * skl2;
-            const char* vt = (const char*)vbase + key0 * svl2;
             if (!I8) {
 #pragma unroll
                 for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + wq) * 1024);
@@ -188,11 +192,18 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 #pragma unroll
             for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
         } else {
+            // The tile's base stays in SGPRs; the lane's row (clamped to Lk - 1) enters through its 32-bit offset. The
+            // lane id is read again here (a volatile read the compiler cannot hoist), so that this branch, taken once,
+            // holds no registers across the tile loop.
+            u32 ln;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+            const int r0 = 4 * wq + (int)(ln >> 4);
+            const u32 kcl = ((ln & 15) ^ (u32)r0) << 4, vcl = ((ln & 15) ^ ((ln >> 4) << 2)) << 4;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                const int key = min(key0 + 16 * i + row0, p.Lk - 1);
-                if (!I8) dma16_at(kbase + (long)key * p.skl + kc * 8, st + (4 * i + wq) * 1024);
-                dma16_at(vbase + (long)key * p.svl + vc * 8, st + T::K_BYTES + (4 * i + wq) * 1024);
+                const u32 r = (u32)(min(key0 + 16 * i + r0, p.Lk - 1) - key0);
+                if (!I8) dma16(kt, r * (u32)skl2 + kcl, st + (4 * i + wq) * 1024);
+                dma16(vt, r * (u32)svl2 + vcl, st + T::K_BYTES + (4 * i + wq) * 1024);
             }
         }
     };
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // LDS offsets of the lane's V^T reads (and int8 K reads) within a stage, fixed for the whole loop: the stage
     // enters as an immediate offset (the loop below is unrolled over the two stages), so the tile loop spends
     // no VALU on them. Kept opaque so that the compiler holds them in VGPRs rather than recomputing them.
-    u32 k_rd[4], v_rd[4];
+    u32 k_rd[4];
     u32 ks_rd = 0;
     if (I8) {
 #pragma unroll
@@ -208,91 +219,98 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         ks_rd = (u32)(KB * 128 + 16 * g);
         asm volatile("" : "+v"(ks_rd));
     }
-    const u32 smem_u = lds_addr(smem);  // the dynamic LDS base, folded into the per-lane offsets below
+    const u32 smem_u = lds_addr(smem);  // the dynamic LDS base (0: no static LDS), folded into the per-lane offsets below
+    // V^T reads: chunk 4 dt + c' of the lane's rows sits at 4 dt ^ vx, so its offset is v_base ^ 64 dt (v_base has
+    // zeros in bits 4-7 besides vx << 4, and the stage's K part is a whole number of 256-byte rows).
+    u32 v_base;
     {
         const int sg = lane & 15;
         const u32 vt = smem_u + (u32)(T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
-        const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);  // chunk 4 dt + c' sits at 4 dt ^ vx
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++) v_rd[dt] = vt + (u32)(((4 * dt) ^ vx) << 4);
+        const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);
+        v_base = vt + (u32)(vx << 4);
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
         if (I8) asm volatile("" : "+v"(k_rd[i]));
-#pragma unroll
-    for (int i = 0; i < 4; i++) asm volatile("" : "+v"(v_rd[i]));
+    asm volatile("" : "+v"(v_base));
 
     // The fp16 K reads of a lane: row lq of the stage, chunk 2 ks + g at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx, i.e. byte
-    // offset ((kx << 4) ^ 32 ks) + 256 lq -- one xor-add per read from two values held for the whole loop.
-    u32 k_row = smem_u + (u32)(lq * 256), k_x16 = (u32)(((lane & 15) ^ g) << 4);
-    asm volatile("" : "+v"(k_row), "+v"(k_x16));
+    // offset 256 lq + ((kx << 4) ^ 32 ks). The dynamic LDS starts at offset 0 (this kernel has no static LDS), so the
+    // low eight bits of k_base are kx << 4 and the read for ks is k_base ^ 32 ks: one xor per read from one value.
+    u32 k_base = smem_u + (u32)(lq * 256) + (u32)(((lane & 15) ^ g) << 4);
+    asm volatile("" : "+v"(k_base));
 
-    // S^T of the tile in stage ST (scaled for int8), into s.
-    float s[16];
-    auto scores = [&](auto stage) __attribute__((always_inline)) {
-        const char* st = smem + decltype(stage)::value * T::BYTES;
-        constexpr u32 st_u = decltype(stage)::value * T::BYTES;  // the stage: an immediate offset of the reads
-        if (!I8) {
-            // K operands in two batches of four reads; each batch goes out before the products that use it. The row
-            // offset passes through an empty asm in every tile, so the eight addresses are made where they are read
-            // (one xor-add each) rather than hoisted out of the loop into eight more VGPRs.
-            u32 kr = k_row;
-            asm volatile("" : "+v"(kr));
+    // S^T of the tile in stage `stage` (a compile-time stage folds into the reads' offset fields; a runtime one is
+    // added), scaled for int8, into out. hook(k) runs right after the k-th product is issued (eight fp16 products,
+    // four int8 ones): the caller puts the previous tile's exponentials there, which the transcendental unit runs
+    // while the matrix cores work on these products.
+    auto qk = [&](auto stage, float (&out)[16], auto&& hook) __attribute__((always_inline)) {
+        const u32 st_u = (u32)((int)stage * T::BYTES);
+        if constexpr (!I8) {
+            // K operands of the first 64 dims go out before the products; each operand of the second 64 is read into
+            // the registers the matching first-half product has just consumed. The base passes through an empty asm
+            // in every tile, so the eight addresses are made where they are read (one xor each) rather than hoisted
+            // out of the loop into eight more VGPRs.
+            u32 kb = k_base;
+            asm volatile("" : "+v"(kb));
             f16v acc = {};
+            h8 ka[4];
 #pragma unroll
-            for (int half_k = 0; half_k < 2; half_k++) {
-                h8 ka[4];
+            for (int k4 = 0; k4 < 4; k4++) ka[k4] = lds_h8((kb ^ (u32)(32 * k4)) + st_u);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int k4 = 0; k4 < 4; k4++) ka[k4] = lds_h8(((k_x16 ^ (u32)(32 * (half_k * 4 + k4))) + kr) + st_u);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int k4 = 0; k4 < 4; k4++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4], qf[half_k * 4 + k4], acc, 0, 0, 0);
+            for (int k4 = 0; k4 < 4; k4++) {
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4], qf[k4], acc, 0, 0, 0);
+                ka[k4] = lds_h8((kb ^ (u32)(32 * (4 + k4))) + st_u);
+                hook(k4);
                 __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = acc[r];
+            for (int k4 = 0; k4 < 4; k4++) {
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[k4], qf[4 + k4], acc, 0, 0, 0);
+                hook(4 + k4);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) out[r] = acc[r];
         } else {
             i4v ka[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(st + k_rd[ks]);
+            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(smem + st_u + k_rd[ks]);
             __builtin_amdgcn_sched_barrier(0);
             i16v acc = {};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
+            for (int ks = 0; ks < 4; ks++) {
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
+                hook(ks);
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++) {
-                const f4 sc = *(const f4*)(st + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
+                const f4 sc = *(const f4*)(smem + st_u + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
 #pragma unroll
-                for (int e = 0; e < 4; e++) s[r4 * 4 + e] = (float)acc[r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
+                for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
             }
         }
     };
-    // Masking (mask: the tile may reach past Lk) and the online softmax for the tile at key0, from s: updates
-    // m, l and O's scale and leaves P in pf.
-    h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
-    auto softmax = [&](int key0, auto mask) {
-        // Keys past Lk (hip_attention.hip:324-328).
-        if (decltype(mask)::value && key0 + KB > p.Lk) {
+    auto no_hook = [](int) {};
+    // Keys past Lk (hip_attention.hip:324-328): only the last tile can reach past Lk.
+    auto mask = [&](float (&x)[16], int key0) __attribute__((always_inline)) {
+        if (key0 + KB > p.Lk) {
 #pragma unroll
             for (int r = 0; r < 16; r++)
-                if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) s[r] = -1e30f;
+                if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) x[r] = -1e30f;
         }
-        float mx = max3(s[0], s[1], s[2]);
+    };
+
+    // The online softmax of a tile with scores s: P = exp2(s * scale_log2 - m) (int8: exp2(s - m)), rounded to fp16 into
+    // pf, and l += the fp16 P (in fp32, by v_dot2 with ones). `exps(k)` does the k-th of eight (int8: four) equal parts.
+    float s[16];
+    h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
+    constexpr int PARTS = I8 ? 4 : 8, PER = 16 / PARTS;
+    auto exps = [&](int k) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 3; r < 15; r += 2) mx = max3(mx, s[r], s[r + 1]);
-        mx = max3(mx, s[15], s[15]);
-        const f2 mh = halves(mx);
-        mx = max3(mh[0], mh[1], mh[1]);
-        if (!I8) mx *= p.scale_log2;
-        if (__any(mx > m + 8.f)) {
-            const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
-            m = mn;
-            l *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] *= alpha;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
+        for (int r = k * PER; r < (k + 1) * PER; r += 2) {
             const float e0 = I8 ? __builtin_amdgcn_exp2f(s[r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.scale_log2, -m));
             const float e1 = I8 ? __builtin_amdgcn_exp2f(s[r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], p.scale_log2, -m));
             const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
@@ -301,61 +319,127 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             pf[r >> 3][(r & 7) + 1] = pk[1];
         }
     };
-    // O^T += V^T P^T with the V tile of stage ST and P in pf; the second step's V^T operands are read while the
-    // first step's products run.
-    auto pv = [&](auto stage) __attribute__((always_inline)) {
-        constexpr u32 st_u = decltype(stage)::value * T::BYTES;
-        auto read_v = [&](h8 (&va)[4], int j) __attribute__((always_inline)) {
+    // The lazy rescale (hip_attention.hip:333-340): m moves only when some row's tile maximum exceeds m + 8. The tile's P
+    // is first made with the current m; a row whose maximum exceeds m + 8 has a P of at least ~2^7.8 in one of its two
+    // lanes, so a lane sum that grew by no more than 64 (and is not NaN) proves that no row needs the rescale, and the
+    // P just made is the one the rule gives. Otherwise (always on the first tile, where m is -1e30 and P overflows,
+    // rarely after) the scores are recomputed from the tile still in LDS, the rule is applied to their maxima, and P
+    // and l are made again from the old l -- the same values, in the same order, as applying the rule first.
+    auto settle = [&](auto stage, int key0, auto last, float l_old) __attribute__((always_inline)) {
+        if (__builtin_expect(__any(!(l <= l_old + 64.f)), 0)) {
+            qk(stage, s, no_hook);
+            if constexpr (decltype(last)::value) mask(s, key0);
+            // The maximum reads the products' results through compiler-visible operations: the compiler inserts
+            // the wait states a VALU read of an MFMA result needs only for instructions it can see, not inline asm.
+            float mx = s[0];
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const u32 ra = v_rd[dt] + st_u + 16 * j * 256;
-                va[dt] = __builtin_shufflevector(read_tr(ra), read_tr(ra + 8 * 256), 0, 1, 2, 3, 4, 5, 6, 7);
+            for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[r]);
+            const f2 mh = halves(mx);
+            mx = fmaxf(mh[0], mh[1]);
+            if (!I8) mx *= p.scale_log2;
+            l = l_old;
+            if (__any(mx > m + 8.f)) {
+                const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);
+                m = mn;
+                l *= alpha;
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] *= alpha;
             }
+#pragma unroll
+            for (int k = 0; k < PARTS; k++) exps(k);
+        }
+    };
+    // O^T += V^T P^T with the V tile of stage `stage` and P in pf. Each V^T operand of the second 16-key step is read
+    // into the registers the matching first-step product has just consumed.
+    auto pv = [&](auto stage) __attribute__((always_inline)) {
+        const u32 st_u = (u32)((int)stage * T::BYTES);
+        u32 vb = v_base;
+        asm volatile("" : "+v"(vb));
+        auto read_v = [&](int j, int dt) __attribute__((always_inline)) {
+            const u32 ra = (vb ^ (u32)(64 * dt)) + st_u + 16 * j * 256;
+            return __builtin_shufflevector(read_tr(ra), read_tr(ra + 8 * 256), 0, 1, 2, 3, 4, 5, 6, 7);
         };
-        h8 va[2][4];
-        read_v(va[0], 0);
-        read_v(va[1], 1);
+        h8 va[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) va[dt] = read_v(0, dt);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int dt = 0; dt < 4; dt++) {
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], pf[0], o[dt], 0, 0, 0);
+            va[dt] = read_v(1, dt);
+            __builtin_amdgcn_sched_barrier(0);
+        }
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[j][dt], pf[j], o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], pf[1], o[dt], 0, 0, 0);
     };
 
-    // Tile loop: the copies of tile i + 1 go out before the work on tile i and are awaited at its closing
-    // barrier, which also retires every read of the stage the next copies overwrite. Unrolled over the two
-    // stages. The last tile -- the only one that can reach past Lk -- is peeled off with the masking (under a
-    // runtime test the compiler turns the masking into selects on every tile).
+    // Tile loop, software-pipelined over three LDS stages. At the start of step i, tiles i and i + 1 are in LDS and
+    // s holds tile i's scores. Step i issues the copies of tile i + 2 (into the stage tile i - 1 left), computes
+    // tile i + 1's scores with tile i's exponentials between the products, settles the rescale, runs tile i's PV
+    // product, and awaits tile i + 2 at the barrier closing the step (which also retires every read of tile i's
+    // stage before step i + 1 copies into it). Tile t sits in stage (t - tiles + 1) mod 3, so the last tile is in
+    // stage 0 and the one before it in stage 2. The steady steps run six to a loop pass -- stages 2, 0, 1 twice,
+    // which also returns the scores to the registers they started in (they alternate between two sets) -- after
+    // 0-5 steps taken one at a time with the stage at run time. Kinds: 0 = steady; 1 = the step before the last
+    // (next tile masked, nothing to copy); 2 = the last.
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    auto tile = [&](int i, auto stage, auto last) __attribute__((always_inline)) {
-        if constexpr (!decltype(last)::value) issue((i + 1) * KB, smem + (decltype(stage)::value ^ 1) * T::BYTES);
-        scores(stage);
-        softmax(i * KB, last);
-        pv(stage);
-        if constexpr (!decltype(last)::value) {
+    using S2 = std::integral_constant<int, 2>;
+    using Steady = std::integral_constant<int, 0>;
+    using Penult = std::integral_constant<int, 1>;
+    using Last = std::integral_constant<int, 2>;
+    auto step = [&](int i, auto stage, auto kind) __attribute__((always_inline)) {
+        constexpr int K = decltype(kind)::value;
+        const auto next = next_stage(stage);
+        if constexpr (K == 0) issue((i + 2) * KB, smem + (int)next_stage(next) * T::BYTES);
+        const float l_old = l;
+        if constexpr (K != 2) {
+            float nxt[16];
+            qk(next, nxt, exps);
+            if constexpr (K == 1) mask(nxt, (i + 1) * KB);
+            settle(stage, i * KB, std::false_type{}, l_old);
+            pv(stage);
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[r] = nxt[r];
+        } else {
+#pragma unroll
+            for (int k = 0; k < PARTS; k++) exps(k);
+            settle(stage, i * KB, std::true_type{}, l_old);
+            pv(stage);
+        }
+        if constexpr (K == 0) {
             wait_copies();
             __syncthreads();
         }
     };
-    // Tile i uses stage (tiles - 1 - i) & 1, so the last tile is always in stage 0 and the loop runs in whole pairs.
-    int i = 0;
-    if (tiles % 2 == 0) {
-        issue(0, smem + T::BYTES);
-        wait_copies();
-        __syncthreads();
-        tile(0, S1{}, std::false_type{});
-        i = 1;
+    const int first = ((1 - tiles) % 3 + 3) % 3;  // the stage of tile 0
+    issue(0, smem + first * T::BYTES);
+    if (tiles > 1) issue(KB, smem + next_stage(first) * T::BYTES);
+    wait_copies();
+    __syncthreads();
+    if (tiles == 1) {
+        qk(S0{}, s, no_hook);
+        mask(s, 0);
+        step(0, S0{}, Last{});
     } else {
-        issue(0, smem);
-        wait_copies();
-        __syncthreads();
+        qk(first, s, no_hook);
+        const int steady = tiles - 2, peel = steady % 6;
+        if (peel >= 5) step(peel - 5, S0{}, Steady{});
+        if (peel >= 4) step(peel - 4, S1{}, Steady{});
+        if (peel >= 3) step(peel - 3, S2{}, Steady{});
+        if (peel >= 2) step(peel - 2, S0{}, Steady{});
+        if (peel >= 1) step(peel - 1, S1{}, Steady{});
+        for (int i = peel; i < steady; i += 6) {
+            step(i, S2{}, Steady{});
+            step(i + 1, S0{}, Steady{});
+            step(i + 2, S1{}, Steady{});
+            step(i + 3, S2{}, Steady{});
+            step(i + 4, S0{}, Steady{});
+            step(i + 5, S1{}, Steady{});
+        }
+        step(tiles - 2, S2{}, Penult{});
+        step(tiles - 1, S0{}, Last{});
     }
-    for (; i < tiles - 1; i += 2) {
-        tile(i, S0{}, std::false_type{});
-        tile(i + 1, S1{}, std::false_type{});
-    }
-    tile(tiles - 1, S0{}, std::true_type{});
 
     // Normalise and store: the lane halves hold disjoint keys of one row.
     const f2 lh = halves(l);

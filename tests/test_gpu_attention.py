@@ -34,8 +34,10 @@ def close(out, ref):
 
 
 @pytest.mark.parametrize("int8_qk", [False, True])
+# Key tiles of 32: 2, 10, 32, 1, 128, 33, 3, 5, 6 and 7 -- every count of steps the pipelined tile loop takes one at a
+# time before its six-step passes (0-5), whole and partial last tiles.
 @pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096),
-                                          (1, 2, 1, 200, 1049), (1, 1, 1, 64, 96)])
+                                          (1, 2, 1, 200, 1049), (1, 1, 1, 64, 96), (1, 2, 2, 130, 150), (1, 1, 1, 129, 192), (2, 2, 1, 70, 210)])
 def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
     print(f"attention B={B} H={H} Hkv={Hkv} Lq={Lq} Lk={Lk} int8_qk={int8_qk}", flush=True)
     q, k, v = qkv(B, H, Hkv, Lq, Lk, seed=Lq + Lk)
@@ -63,6 +65,23 @@ def test_attention_large_scores(dev):
     out = torch.empty(1, 2, 200, 128, dtype=torch.float16, device=dev)
     hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5)
     close(out, oracle.attention_f64(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5))
+
+
+@pytest.mark.parametrize("int8_qk", [False, True])
+def test_attention_rising_scores(dev, int8_qk):
+    """Scores that climb along the keys by ~4 (log2 units) per 32-key tile, to ~98 over the row: the running maximum
+    moves every two or three tiles, and most tiles' P sums outgrow the fast path's bound, so they take the path that
+    recomputes the scores and applies the lazy-rescale rule."""
+    B, H, Lq, Lk = 1, 2, 96, 800
+    g = gen(21)
+    q = (torch.rand(B, H, Lq, 128, generator=g) * 0.5 + 0.5).half()
+    ramp = torch.linspace(0.0, 1.0, Lk).view(1, 1, Lk, 1)
+    k = (ramp * 8.0 + torch.randn(B, H, Lk, 128, generator=g) * 0.05).half()
+    v = torch.randn(B, H, Lk, 128, generator=g).half()
+    out = torch.empty(B, H, Lq, 128, dtype=torch.float16, device=dev)
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5, int8_qk)
+    ref = (oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64)(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5)
+    close(out, ref)
 
 
 def test_comfy_backend_strided_layout(dev):
