@@ -562,12 +562,23 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     // One slice. AHEAD: slice kt + NS exists and is copied during this slice's last k step (then slices
     // kt + 2 .. kt + NS - 1 exist too); MORE: slice kt + 1 exists; SI >= 0: kt % NS, known at compile time,
     // so the slice's LDS reads take their stage as an immediate offset.
+    // GROUP_SCALED fold of block p's partial (one group: one slice) into its fp32 sums, with the group scales in gv.
+    // Register r of block (i, j) is column wn TN + 32 j + 8 (r / 4) + 4 g + r % 4.
+    h4v gv[GRP ? FJ : 1][4];
+    auto fold = [&](int p) __attribute__((always_inline)) {
+        const int i = p / FJ, j = p % FJ;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e] =
+                    __builtin_fmaf((float)acc[i][j][4 * q + e], (float)gv[GRP ? j : 0][q][e], yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e]);
+    };
     auto slice = [&](int kt, auto ahead, auto more, auto si) {
         constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
         constexpr int SI = decltype(si)::value;
         const char* st = SI >= 0 ? smem + SI * STAGE : stage(kt);
         const char* sn = SI >= 0 ? smem + (SI + 1) % NS * STAGE : stage(kt + 1);
-        h4v gv[GRP ? FJ : 1][4];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             if (ks == KS - 1) {
@@ -579,13 +590,17 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
             const bool last = ks == KS - 1;
 #pragma unroll
             for (int p = 0; p < NF; p++) {
+                // GROUP_SCALED: the previous slice's partial of block p is folded just before the block's first
+                // product of this slice restarts it, in the shadow of the other blocks' products (issued between
+                // them), rather than all at the end of the slice with the matrix cores idle.
+                if (GRP && ks == 0 && kt > 0) fold(p);
                 const i16v c0 = GRP && ks == 0 ? (i16v){} : acc[p / FJ][p % FJ];
                 acc[p / FJ][p % FJ] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fr[cur][FI + p % FJ], fr[cur][p / FJ], c0, 0, 0, 0);
                 if (AHEAD && ks == KS - 1)
 #pragma unroll
                     for (int c = 0; c < NI; c++)
                         if (c * NF / NI == p) copy(kt + NS, c);
-                if (GRP && ks == 0 && p == 0)
+                if (GRP && ks == 0 && p == NF - 1)  // this slice's scales, once the previous slice's are used
 #pragma unroll
                     for (int j = 0; j < FJ; j++)
 #pragma unroll
@@ -603,20 +618,6 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-        }
-        if constexpr (GRP) {
-            // Fold the slice's partials: register r of block (i, j) is column wn TN + 32 j + 8 (r / 4) + 4 g + r % 4.
-#pragma unroll
-            for (int j = 0; j < FJ; j++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-#pragma unroll
-                    for (int i = 0; i < FI; i++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e] =
-                                __builtin_fmaf((float)acc[i][j][4 * q + e], (float)gv[GRP ? j : 0][q][e], yacc[GRP ? i : 0][GRP ? j : 0][4 * q + e]);
-                }
         }
     };
     using yes = std::integral_constant<bool, true>;
@@ -638,6 +639,9 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     for (; kt + NS < KT; kt++) slice(kt, yes{}, yes{}, any{});
     for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{}, any{});
     slice(kt, no{}, no{}, any{});
+    if constexpr (GRP)  // the last slice's partials
+#pragma unroll
+        for (int p = 0; p < NF; p++) fold(p);
     if constexpr (W4) {  // the int4 operands were 16 times their values: undo it (exactly)
         if constexpr (GRP) {
 #pragma unroll
