@@ -81,7 +81,10 @@ def test_attention_decode(dev, B, H, Hkv, cap, lengths):
     assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
 
 
-@pytest.mark.parametrize("shape", [(1, 4096, 3072), (2, 3, 50, 128), (1, 7, 64), (1, 5, 8192), (2, 9, 136)])
+# D > 128: one wave per row, 1-4 steps per slot (D = 136 .. 8192, chunk counts that leave slots and steps partly or
+# wholly empty), row counts that leave a workgroup's last waves without a row; D <= 128: 16 lanes per row.
+@pytest.mark.parametrize("shape", [(1, 4096, 3072), (2, 3, 50, 128), (1, 7, 64), (1, 5, 8192), (2, 9, 136), (1, 3, 5120), (3, 2, 2048),
+                                   (1, 6, 4104), (1, 1, 1032)])
 def test_rms_norm_bit_exact(dev, shape):
     print(f"rms_norm {shape}", flush=True)
     g = gen(10)
@@ -92,9 +95,10 @@ def test_rms_norm_bit_exact(dev, shape):
     assert_same(bits(out), bits(oracle.rms_norm(x.numpy(), w.numpy(), 1e-6)))
 
 
-def test_rms_norm_strided_heads(dev):
+@pytest.mark.parametrize("D", [128, 256])
+def test_rms_norm_strided_heads(dev, D):
     """(B, H, L, D) views of a (B, L, H*D) buffer: the kernel reads with strides, writes contiguous (B, H, L, D)."""
-    B, L, H, D = 2, 33, 4, 128
+    B, L, H = 2, 33, 4
     g = gen(11)
     base = torch.randn(B, L, H * D, generator=g).half()
     w = (torch.randn(D, generator=g) * 0.1).float()
