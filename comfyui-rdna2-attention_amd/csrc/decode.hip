@@ -264,44 +264,59 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     for (int base = begin + wave * PW; base < end; base += W * PW) {
         f4 kr[ITS][2], vr[ITS][2];
         bool valid[ITS];
+        // Loads in the order the two halves of the round use them (K then V of steps 0-1, then of steps 2-3), so the
+        // first half's arithmetic waits only for its own data and runs while the second half's arrives.
 #pragma unroll
-        for (int it = 0; it < ITS; it++) {
-            const int j = base + it * 4 + pos;
-            valid[it] = j < end;
-            const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
-            kr[it][0] = *(const f4*)(k + row);
-            kr[it][1] = *(const f4*)(k + row + 4);
-            vr[it][0] = *(const f4*)(v + row);
-            vr[it][1] = *(const f4*)(v + row + 4);
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int it = half * ITS / 2; it < (half + 1) * ITS / 2; it++) {
+                const int j = base + it * 4 + pos;
+                valid[it] = j < end;
+                const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
+                kr[it][0] = *(const f4*)(k + row);
+                kr[it][1] = *(const f4*)(k + row + 4);
+            }
+#pragma unroll
+            for (int it = half * ITS / 2; it < (half + 1) * ITS / 2; it++) {
+                const int j = base + it * 4 + pos;
+                const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
+                vr[it][0] = *(const f4*)(v + row);
+                vr[it][1] = *(const f4*)(v + row + 4);
+            }
         }
 #pragma unroll
-        for (int g = 0; g < REP; g++) {
-            float s[ITS];
-            float top = -1e30f;
+        for (int half = 0; half < 2; half++)
 #pragma unroll
-            for (int it = 0; it < ITS; it++) {
-                const f4 d = qv[g][0] * kr[it][0] + qv[g][1] * kr[it][1];
-                const float x = row_sum16((d[0] + d[1]) + (d[2] + d[3]));
-                s[it] = valid[it] ? x : -1e30f;
-                top = fmaxf(top, s[it]);
-            }
-            top = rows_max(top);
-            const float next = fmaxf(mx[g], top), keep = __expf(mx[g] - next);
-            float psum = 0.f;
-            f4 a0 = acc[g][0] * keep, a1 = acc[g][1] * keep;
+            for (int g = 0; g < REP; g++) {
+                constexpr int HI = ITS / 2;
+                float s[HI];
+                float top = -1e30f;
 #pragma unroll
-            for (int it = 0; it < ITS; it++) {
-                const float p = valid[it] ? __expf(s[it] - next) : 0.f;
-                psum += p;
-                a0 += vr[it][0] * p;
-                a1 += vr[it][1] * p;
+                for (int u = 0; u < HI; u++) {
+                    const int it = half * HI + u;
+                    const f4 d = qv[g][0] * kr[it][0] + qv[g][1] * kr[it][1];
+                    const float x = row_sum16((d[0] + d[1]) + (d[2] + d[3]));
+                    s[u] = valid[it] ? x : -1e30f;
+                    top = fmaxf(top, s[u]);
+                }
+                top = rows_max(top);
+                const float next = fmaxf(mx[g], top), keep = __expf(mx[g] - next);
+                float psum = 0.f;
+                f4 a0 = acc[g][0] * keep, a1 = acc[g][1] * keep;
+#pragma unroll
+                for (int u = 0; u < HI; u++) {
+                    const int it = half * HI + u;
+                    const float p = valid[it] ? __expf(s[u] - next) : 0.f;
+                    psum += p;
+                    a0 += vr[it][0] * p;
+                    a1 += vr[it][1] * p;
+                }
+                psum = rows_sum(psum);
+                sum[g] = sum[g] * keep + psum;
+                acc[g][0] = a0;
+                acc[g][1] = a1;
+                mx[g] = next;
             }
-            psum = rows_sum(psum);
-            sum[g] = sum[g] * keep + psum;
-            acc[g][0] = a0;
-            acc[g][1] = a1;
-            mx[g] = next;
-        }
     }
     // The four position groups of the wave hold partial sums of the same dims: add them up.
 #pragma unroll
@@ -344,16 +359,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 }
 
 // attn_merge (int8_gemv.hip:182-195): joins the splits, one block per query head.
+// Every load -- the splits' (max, sum) pairs and the thread's partial of each split -- is issued before any
+// arithmetic, so the merge is one memory round trip rather than two.
 __global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restrict__ partial, const float* __restrict__ stats, float* __restrict__ out) {
     const size_t head = blockIdx.x;
-    const float* st = stats + head * SPLITS * 2;
-    float top = st[0];
-    for (int s = 1; s < SPLITS; s++) top = fmaxf(top, st[s * 2]);
+    const f2* st = (const f2*)(stats + head * SPLITS * 2);
+    f2 ms[SPLITS];
+    float pv[SPLITS];
+#pragma unroll
+    for (int s = 0; s < SPLITS; s++) ms[s] = st[s];
+#pragma unroll
+    for (int s = 0; s < SPLITS; s++) pv[s] = partial[(head * SPLITS + s) * HEAD + threadIdx.x];
+    float top = ms[0][0];
+#pragma unroll
+    for (int s = 1; s < SPLITS; s++) top = fmaxf(top, ms[s][0]);
     float value = 0.f, total = 0.f;
+#pragma unroll
     for (int s = 0; s < SPLITS; s++) {
-        const float keep = __expf(st[s * 2] - top);
-        value += partial[(head * SPLITS + s) * HEAD + threadIdx.x] * keep;
-        total += st[s * 2 + 1] * keep;
+        const float keep = __expf(ms[s][0] - top);
+        value += pv[s] * keep;
+        total += ms[s][1] * keep;
     }
     out[head * HEAD + threadIdx.x] = value / total;
 }
