@@ -381,24 +381,32 @@ def w_dit_block(torch, dev):
 CALIB_BLOCKS, CALIB_ITERS = 2048, 2000
 
 
-def w_mfma_peak(torch, dev, int8):
-    """Back-to-back independent MFMAs on every SIMD (csrc/calib.hip): the matrix rate this GPU sustains."""
+def w_mfma_peak(torch, dev, int8, random=False):
+    """Back-to-back independent MFMAs on every SIMD (csrc/calib.hip): the matrix rate this GPU sustains. random: the
+    operands are N(0, 1) fp16 or uniform int8 values (the clock, and so the rate, settles lower on random data)."""
     from comfyui_rdna2_attention_amd import _lib
     out = torch.empty(CALIB_BLOCKS * 256, dtype=torch.int32, device=dev)
     clocks = torch.zeros(2, dtype=torch.int64, device=dev)
     lib = _lib.load()
-    fn = lambda i: _lib.check(lib.rda_calib_mfma_peak(int(int8), CALIB_BLOCKS, CALIB_ITERS, _lib.ptr(out), _lib.ptr(clocks), _lib.stream()))  # noqa: E731
+    if random:
+        n = CALIB_BLOCKS * 256 * 16 * 16  # 16 fragments of 16 bytes per lane
+        g = gen(torch, 30)
+        ops = (torch.randint(-128, 128, (n,), generator=g, dtype=torch.int8) if int8 else torch.randn(n // 2, generator=g).half()).to(dev)
+        fn = lambda i: _lib.check(lib.rda_calib_mfma_peak_data(int(int8), CALIB_BLOCKS, CALIB_ITERS, _lib.ptr(ops), _lib.ptr(out), _lib.ptr(clocks),  # noqa: E731
+                                                              _lib.stream()))
+    else:
+        fn = lambda i: _lib.check(lib.rda_calib_mfma_peak(int(int8), CALIB_BLOCKS, CALIB_ITERS, _lib.ptr(out), _lib.ptr(clocks), _lib.stream()))  # noqa: E731
     fn.clocks = clocks
     work = CALIB_BLOCKS * 4.0 * CALIB_ITERS * 8 * (65536 if int8 else 32768)
     return fn, 1, work, "mfma_i8" if int8 else "mfma_f16", event_timed
 
 
 def calibrate(torch, dev, steps, warmup):
-    """Measured MFMA peaks (int8, fp16) and the shader clock they ran at (shader-clock ticks over 100 MHz real-time
-    ticks of one wave)."""
+    """Measured MFMA peaks (int8, fp16; on fixed small-integer operands and on random ones) and the shader clock they
+    ran at (shader-clock ticks over 100 MHz real-time ticks of one wave)."""
     res = {}
-    for name, int8 in (("mfma_i8", True), ("mfma_f16", False)):
-        fn, _, work, bound, timer = w_mfma_peak(torch, dev, int8)
+    for name, int8, random in (("mfma_i8", True, False), ("mfma_f16", False, False), ("mfma_i8_random", True, True), ("mfma_f16_random", False, True)):
+        fn, _, work, bound, timer = w_mfma_peak(torch, dev, int8, random)
         _, kms = timer(torch, fn, steps, warmup)
         ticks, rt = (int(v) for v in fn.clocks.cpu())
         peak = PEAKS[bound][1]
@@ -437,14 +445,17 @@ WORKLOADS = {
     "copy": w_copy,
     "mfma_peak_i8": lambda t, d: w_mfma_peak(t, d, True),
     "mfma_peak_f16": lambda t, d: w_mfma_peak(t, d, False),
+    "mfma_peak_i8_random": lambda t, d: w_mfma_peak(t, d, True, True),
+    "mfma_peak_f16_random": lambda t, d: w_mfma_peak(t, d, False, True),
 }
-NOT_COMPONENTS = ("attention_f16", "copy", "mfma_peak_i8", "mfma_peak_f16")
+NOT_COMPONENTS = ("attention_f16", "copy", "mfma_peak_i8", "mfma_peak_f16", "mfma_peak_i8_random", "mfma_peak_f16_random")
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}
 # The roofline of each workload (the 4th item its function returns), for the CPU leg, which runs without a GPU.
 WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
                   "w4a8_gemm": "mfma_i8", "w4a8_gemm_k12288": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
                   "decode_gemv_n1024": "hbm", "decode_gemv_n12288": "hbm", "decode_attention": "hbm", "decode_layer": "hbm", "dit_block": "mfma_i8",
-                  "copy": "hbm", "mfma_peak_i8": "mfma_i8", "mfma_peak_f16": "mfma_f16"}
+                  "copy": "hbm", "mfma_peak_i8": "mfma_i8", "mfma_peak_f16": "mfma_f16", "mfma_peak_i8_random": "mfma_i8",
+                  "mfma_peak_f16_random": "mfma_f16"}
 
 
 def run_workload(torch, dev, name, steps, warmup, traffic):
@@ -696,7 +707,13 @@ def main():
     if not args.no_components:
         result["components"] = {name: run_workload(torch, dev, name, args.steps, args.warmup, traffic)
                                 for name in WORKLOADS if name not in NOT_COMPONENTS}
-        result["calibration"] = calibrate(torch, dev, args.steps, args.warmup)
+        cal = result["calibration"] = calibrate(torch, dev, args.steps, args.warmup)
+        # The same achieved rates against the matrix rate measured on random operands (the power-bound ceiling).
+        sustained = {"mfma_f16": cal["mfma_f16_random"]["value"], "mfma_i8": cal["mfma_i8_random"]["value"]}
+        result["frac_of_random_operand_peak"] = round(result["value"] / sustained["mfma_f16"], 4)
+        for name, rec in result["components"].items():
+            if WORKLOAD_BOUND[name] in sustained:
+                rec["frac_of_random_operand_peak"] = round(rec["value"] / sustained[WORKLOAD_BOUND[name]], 4)
     if not args.no_cpu:
         # The headline's sample is larger (6 of 24 heads, about 10 s); each component's is about 1.5 s.
         result["cpu_baseline"] = cpu_baseline(torch, "attention_f16", seconds=10.0, heads=6)

@@ -42,6 +42,7 @@ SIGNATURES = {
     "rda_decode_splits": (_i, []),
     "rda_attention_decode_noalloc": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p]),
     "rda_calib_mfma_peak": (_i, [_i, _i, _i, _p, _p, _p]),
+    "rda_calib_mfma_peak_data": (_i, [_i, _i, _i, _p, _p, _p, _p]),
     "rda_rms_norm_head": (_i, [_p, _p, _p, _i, _i, _i, _i, _l, _l, _l, _f, _p]),
     "rda_rms_norm_row": (_i, [_p, _p, _p, _i, _i, _i, _i, _l, _l, _l, _f, _p]),
     "rda_rms_norm_rope": (_i, [_p, _p, _p, _i, _i, _i, _i, _l, _l, _l, _f, _p, _l, _p]),

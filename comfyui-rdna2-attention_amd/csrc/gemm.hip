@@ -300,7 +300,7 @@ __device__ __forceinline__ void epilogue_rows(const i16v (&acc)[FI][FJ], int lan
 // 128-byte lines (the register layout would touch 32 rows per instruction). R and G are read the same way.
 // Bytes of the bias area of the scale block: BN halfs, copied in 256-byte instructions.
 constexpr int SC_BIAS(int bn) { return (bn * 2 + 255) / 256 * 256; }
-template <int BM, int BN, int FI, int FJ, int EPI>
+template <int BM, int BN, int FI, int FJ, int EPI, int NT>
 __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const f16v (&yacc)[EPI == GROUP_SCALED ? FI : 1][EPI == GROUP_SCALED ? FJ : 1],
                                                char* tile, const char* sc, int t, int lane, int wm, int wn, int m0, int n0, int M, int N,
                                                const float* __restrict__ as, const float* __restrict__ ws, const half_t* __restrict__ bias,
@@ -337,15 +337,15 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
                 }
             }
     };
-    constexpr int ITER = BM * CPR / GT;  // 16-byte chunks per thread (the tile is a whole number of them)
-    static_assert(BM * CPR % GT == 0, "whole chunks per thread");
+    constexpr int ITER = BM * CPR / NT;  // 16-byte chunks per thread (the tile is a whole number of them)
+    static_assert(BM * CPR % NT == 0, "whole chunks per thread");
     if (!R) {
         if (bias) dequantize(std::integral_constant<bool, true>{});
         else dequantize(std::integral_constant<bool, false>{});
         __syncthreads();
 #pragma unroll 4
         for (int it = 0; it < ITER; it++) {
-            const int idx = t + it * GT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
+            const int idx = t + it * NT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
             if (m < M) *(h8*)(C + (size_t)m * N + n0 + c) = *(const h8*)(tile + r * TP + c * 2);
         }
         return;
@@ -359,7 +359,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
     auto load = [&](int b, int slot) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < RB; k++) {
-            const int idx = t + (b * RB + k) * GT, r = idx / CPR, c = (idx % CPR) * 8, m = min(m0 + r, M - 1);
+            const int idx = t + (b * RB + k) * NT, r = idx / CPR, c = (idx % CPR) * 8, m = min(m0 + r, M - 1);
             res[slot][k] = *(const h8*)(R + (size_t)m * N + n0 + c);
             gat[slot][k] = *(const h8*)(G + (size_t)(m / L) * N + n0 + c);
         }
@@ -373,7 +373,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
         if (b + 1 < NBATCH) load(b + 1, (b + 1) & 1);
 #pragma unroll
         for (int k = 0; k < RB; k++) {
-            const int idx = t + (b * RB + k) * GT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
+            const int idx = t + (b * RB + k) * NT, r = idx / CPR, c = (idx % CPR) * 8, m = m0 + r;
             h8 y = *(const h8*)(tile + r * TP + c * 2);
 #pragma unroll
             for (int e = 0; e < 8; e++) y[e] = to_half((float)res[b & 1][k][e] + r16((float)gat[b & 1][k][e] * (float)y[e]));
@@ -406,20 +406,21 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 // copy and fragment read is issued in the shadow of a product, spread evenly over its 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM>
-__global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM, int NW>
+__global__ __launch_bounds__(64 * NW, MINB) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
                                                       const float* __restrict__ ws, const half_t* __restrict__ gs, const half_t* __restrict__ bias,
                                                       void* __restrict__ Cout, int M, int N, int K, const half_t* __restrict__ R,
                                                       const half_t* __restrict__ G, int L) {
-    constexpr int WGN = 4 / WGM, TM = BM / WGM, TN = BN / WGN, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
+    constexpr int NT = 64 * NW, WGN = NW / WGM, TM = BM / WGM, TN = BN / WGN, FI = TM / 32, FJ = TN / 32, NF = FI * FJ, NR = FI + FJ;
     constexpr bool GRP = EPI == GROUP_SCALED;
     constexpr int KS = KB8 / 32;                                      // 32-wide k steps per slice
     constexpr int CPR = KB8 / 16, RPI = 1024 / KB8, RPL = 256 / KB8;  // A rows: chunks per row, rows per copy, rows per bank line
     constexpr int WB = W4 ? KB8 / 2 : KB8;                            // W row bytes per slice
     constexpr int CPRB = WB / 16, RPIB = 1024 / WB, RPLB = 256 / WB;
     constexpr int STAGE = BM * KB8 + BN * WB;
-    constexpr int AI = BM / (4 * RPI), BI = BN / (4 * RPIB), NI = AI + BI;  // copy instructions per wave per slice
-    static_assert((BM == 256 || BM == 128) && (WGM == 1 || WGM == 2) && BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (4 * RPIB) == 0, "tile");
+    constexpr int AI = BM / (NW * RPI), BI = BN / (NW * RPIB), NI = AI + BI;  // copy instructions per wave per slice
+    static_assert((BM == 256 || BM == 128) && (WGM == 1 || WGM == 2) && NW % WGM == 0 && BN % 64 == 0 && TN % 32 == 0 && (KB8 == 64 || KB8 == 128) && BN % (NW * RPIB) == 0 &&
+                  BM % (NW * RPI) == 0, "tile");
     static_assert(!GRP || KB8 == 128, "one group per slice");
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
@@ -452,8 +453,8 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     u32 aoff[AI];
 #pragma unroll
     for (int c = 0; c < AI; c++) {
-        arow[c] = min(m0 + 4 * RPI * c, M - 1);
-        aoff[c] = (u32)(min(m0 + 4 * RPI * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
+        arow[c] = min(m0 + NW * RPI * c, M - 1);
+        aoff[c] = (u32)(min(m0 + NW * RPI * c + crow, M - 1) - arow[c]) * K + cchunk * 16;
     }
     auto stage = [&](int kt) -> const char* { return smem + (kt % NS) * STAGE; };
     // The epilogue's scales go to a scale block: ws[n0 .. n0 + BN) (BN / 64 copies of 64 floats), bias[n0 ..)
@@ -465,7 +466,7 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
         constexpr int NWS = EPI == PER_CHANNEL ? BN / 64 : 0, NB = SC_BIAS(BN) / 256;
 #pragma unroll
         for (int c = 0; c < NWS + NB + BM / 64; c++) {
-            if (c % 4 != wave) continue;
+            if (c % NW != wave) continue;
             if (c < NWS) {
                 dma4(ws + n0 + 64 * c, lane * 4, sc + c * 256);
             } else if (c < NWS + NB) {
@@ -482,15 +483,23 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     half_t* gsl = (half_t*)(smem + GS_OFF);
     if (GRP) {
         const int groups = K / KB8;
-        for (int idx = t; idx < BN * groups; idx += GT) {
-            const int c = idx % BN, gi = idx / BN;
-            gsl[gi * BN + c] = gs[(size_t)(n0 + c) * groups + gi];
+        // The block's scales are BN consecutive rows of gs ([N][groups], contiguous): read them in 16-byte pieces (all
+        // of a thread's pieces in flight together), then transpose them into LDS.
+        const half_t* src = gs + (size_t)n0 * groups;
+        const int pieces = BN * groups / 8;
+        for (int ch = t; ch < pieces; ch += NT) {
+            const h8 v = *(const h8*)(src + (size_t)ch * 8);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int idx = ch * 8 + e, c = idx / groups, gi = idx - c * groups;
+                gsl[gi * BN + c] = v[e];
+            }
         }
     }
     auto copy = [&](int kt, int c) {  // copy instruction c (< NI) of slice kt
         const char* st = stage(kt);
-        if (c < AI) dma16(A + (size_t)arow[c] * K + kt * KB8, aoff[c], st + (4 * c + wave) * 1024);
-        else dma16(W + (size_t)(n0 + 4 * RPIB * (c - AI)) * wrow + kt * WB, boff, st + BM * KB8 + (4 * (c - AI) + wave) * 1024);
+        if (c < AI) dma16(A + (size_t)arow[c] * K + kt * KB8, aoff[c], st + (NW * c + wave) * 1024);
+        else dma16(W + (size_t)(n0 + NW * RPIB * (c - AI)) * wrow + kt * WB, boff, st + BM * KB8 + (NW * (c - AI) + wave) * 1024);
     };
 
     // Fragment f (< FI: A block f, else W block f - FI) of k step kk: row base + lq, k values 32 kk + 16 g ..
@@ -526,6 +535,8 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
         for (int i = 0; i < FI; i++)
 #pragma unroll
             for (int j = 0; j < FJ; j++) yacc[GRP ? i : 0][GRP ? j : 0] = (f16v){};
+    // W4A8 with a wave over 128 rows x 32 columns (four A blocks, one W block) runs the block-major slice below.
+    constexpr bool PIPE = GRP && W4 && FI == 4 && FJ == 1 && KS == 4;
     i4v fr[2][NR];            // fragments of the current and the next k step
     u2v fw[W4 ? FJ : 1];      // packed int4 W fragments of the next k step, before widening
 
@@ -544,7 +555,23 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     else wait_copies();
     __syncthreads();
 #pragma unroll
-    for (int f = 0; f < NR; f++) fr[0][f] = W4 && f >= FI ? widen(wraw(stage(0), 0, f - FI)) : frag(stage(0), 0, f);
+    for (int f = 0; f < NR; f++) {
+        if (PIPE) break;
+        fr[0][f] = W4 && f >= FI ? widen(wraw(stage(0), 0, f - FI)) : frag(stage(0), 0, f);
+    }
+    // PIPE (below): the first three products' A fragments, slice 0's packed W fragments, the first one widened.
+    i4v afr[PIPE ? 4 : 1], wf[PIPE ? 4 : 1];
+    u2v wr[PIPE ? 4 : 1];
+    h4v gva[PIPE ? 4 : 1][4];  // [0]: scales of the slice's blocks 0, 1 fold; [1]: of its blocks 2, 3 (folded in the next slice)
+    if constexpr (PIPE) {
+#pragma unroll
+        for (int P = 0; P < 3; P++) afr[P] = frag(stage(0), (P >> 1) & 3, (P >> 3) * 2 + (P & 1));
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) wr[ks] = wraw(stage(0), ks, 0);
+        wf[0] = widen(wr[0]);
+#pragma unroll
+        for (int q = 0; q < 4; q++) gva[1][q] = (h4v){};  // slice 0 folds the zero partials of blocks 2, 3 with zero scales
+    }
 
     // Copies that may still be in flight at the barrier of slice k once slice k + 1 has landed: the NS - 2
     // slices after it.
@@ -620,6 +647,65 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
             }
         }
     };
+    // PIPE: one slice as 16 products P = 0 .. 15, block-major: block (P / 8) * 2 + P % 2 at k step (P / 2) % 4 (blocks
+    // 0 and 1 alternate over the four k steps, then blocks 2 and 3), so each block's partial is complete eight
+    // products before the block restarts it. Its fold (16 conversions and 16 FMAs) is then spread over those
+    // products, a quarter (8 vector instructions) beside each: blocks 0 and 1 of this slice beside products 8-15,
+    // blocks 2 and 3 of the previous slice beside products 0-7 -- few enough per product that the vector ALU runs
+    // in the matrix cores' shadow (a burst of 32 before a product left the matrix cores idle). A fragments are read
+    // three products ahead (ring of four); the slice's four int4 W fragments are widened once and held, their
+    // packed bytes read after the barrier of the slice before. The barrier sits before product 13, once every read
+    // of the slice's stage has been issued; the copies of slice kt + NS follow it, beside products 13-15. The group
+    // scales are read twice per slice (before product 5 for blocks 0, 1; at 13 for blocks 2, 3), each set then held
+    // until its last fold.
+    auto slice_g = [&](int kt, auto ahead, auto more, auto si) __attribute__((always_inline)) {
+        constexpr bool AHEAD = decltype(ahead)::value, MORE = decltype(more)::value;
+        constexpr int SI = decltype(si)::value;
+        const char* st = SI >= 0 ? smem + SI * STAGE : stage(kt);
+        const char* sn = SI >= 0 ? smem + (SI + 1) % NS * STAGE : stage(kt + 1);
+        const u32 gk = goff + (u32)(kt * BN * 2);
+#pragma unroll
+        for (int P = 0; P < 16; P++) {
+            if (P == 13) {
+                if (AHEAD) wait_copies_but<LEFT>();  // slice kt + 1 has landed
+                else wait_copies();
+                __syncthreads();
+            }
+            const int b = (P >> 3) * 2 + (P & 1), ks = (P >> 1) & 3;
+            const i16v c0 = ks == 0 ? (i16v){} : acc[PIPE ? b : 0][0];
+            acc[PIPE ? b : 0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[PIPE ? ks : 0], afr[PIPE ? P & 3 : 0], c0, 0, 0, 0);
+            {  // a quarter of one block's fold
+                const int fb = P < 8 ? 2 + (P >> 2) : (P - 8) >> 2, q = P & 3, set = P < 8 ? 1 : 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    yacc[PIPE ? fb : 0][0][4 * q + e] =
+                        __builtin_fmaf((float)acc[PIPE ? fb : 0][0][4 * q + e], (float)gva[PIPE ? set : 0][q][e], yacc[PIPE ? fb : 0][0][4 * q + e]);
+            }
+            {  // the A fragment three products ahead
+                const int n = P + 3, nb = ((n & 15) >> 3) * 2 + (n & 1), nk = (n >> 1) & 3;
+                if (n < 16) afr[PIPE ? n & 3 : 0] = frag(st, nk, nb);
+                else if (MORE) afr[PIPE ? n & 3 : 0] = frag(sn, nk, nb);
+            }
+            if (P <= 2) wf[PIPE ? P + 1 : 0] = widen(wr[PIPE ? P + 1 : 0]);  // this slice's k steps 1-3
+            if (MORE && P == 13) {
+                wr[0] = wraw(sn, 0, 0);
+                wr[PIPE ? 1 : 0] = wraw(sn, 1, 0);
+            }
+            if (MORE && P == 14) {
+                wr[PIPE ? 2 : 0] = wraw(sn, 2, 0);
+                wr[PIPE ? 3 : 0] = wraw(sn, 3, 0);
+            }
+            if (MORE && P == 15) wf[0] = widen(wr[0]);  // the next slice's first k step
+            if (P == 5 || P == 13)
+#pragma unroll
+                for (int q = 0; q < 4; q++) gva[PIPE ? (P == 5 ? 0 : 1) : 0][q] = *(const h4v*)(smem + gk + 16 * q);
+            if (AHEAD && P >= 13)
+#pragma unroll
+                for (int c = 0; c < NI; c++)
+                    if (13 + c * 3 / NI == P) copy(kt + NS, c);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     using yes = std::integral_constant<bool, true>;
     using no = std::integral_constant<bool, false>;
     using any = std::integral_constant<int, -1>;
@@ -628,20 +714,31 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
     // starting at a multiple of NS, so slice kt + j is in stage j (18 fewer vector instructions per W4A8
     // slice). With int8 weights the unrolled loop measured the same and ran short of scalar registers.
     static_assert(NS >= 2 && NS <= 4, "stages");
+    auto run = [&](int k, auto ahead, auto more, auto si) __attribute__((always_inline)) {
+        if constexpr (PIPE) slice_g(k, ahead, more, si);
+        else slice(k, ahead, more, si);
+    };
     if constexpr (W4) {
         for (; kt + 2 * NS - 1 < KT; kt += NS) {
-            slice(kt, yes{}, yes{}, std::integral_constant<int, 0>{});
-            slice(kt + 1, yes{}, yes{}, std::integral_constant<int, 1>{});
-            if constexpr (NS > 2) slice(kt + 2, yes{}, yes{}, std::integral_constant<int, 2>{});
-            if constexpr (NS > 3) slice(kt + 3, yes{}, yes{}, std::integral_constant<int, 3>{});
+            run(kt, yes{}, yes{}, std::integral_constant<int, 0>{});
+            run(kt + 1, yes{}, yes{}, std::integral_constant<int, 1>{});
+            if constexpr (NS > 2) run(kt + 2, yes{}, yes{}, std::integral_constant<int, 2>{});
+            if constexpr (NS > 3) run(kt + 3, yes{}, yes{}, std::integral_constant<int, 3>{});
         }
     }
-    for (; kt + NS < KT; kt++) slice(kt, yes{}, yes{}, any{});
-    for (; kt + 1 < KT; kt++) slice(kt, no{}, yes{}, any{});
-    slice(kt, no{}, no{}, any{});
-    if constexpr (GRP)  // the last slice's partials
+    for (; kt + NS < KT; kt++) run(kt, yes{}, yes{}, any{});
+    for (; kt + 1 < KT; kt++) run(kt, no{}, yes{}, any{});
+    run(kt, no{}, no{}, any{});
+    if constexpr (PIPE) {  // the last slice's blocks 2 and 3
+#pragma unroll
+        for (int fb = 2; fb < 4; fb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                yacc[PIPE ? fb : 0][0][r] = __builtin_fmaf((float)acc[PIPE ? fb : 0][0][r], (float)gva[PIPE ? 1 : 0][r >> 2][r & 3], yacc[PIPE ? fb : 0][0][r]);
+    } else if constexpr (GRP) {  // the last slice's partials
 #pragma unroll
         for (int p = 0; p < NF; p++) fold(p);
+    }
     if constexpr (W4) {  // the int4 operands were 16 times their values: undo it (exactly)
         if constexpr (GRP) {
 #pragma unroll
@@ -659,11 +756,11 @@ __global__ __launch_bounds__(GT, MINB) void gemm8_kernel(const int8_t* __restric
         epilogue_rows<FI, FJ, EPI>(acc, lane, m0 + wm * TM, n0 + wn * TN, M, N, as, ws, bias, Cout, R, G, L);
     } else {
         __syncthreads();  // the staged tile overlaps the stages
-        epilogue_block<BM, BN, FI, FJ, EPI>(acc, yacc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
+        epilogue_block<BM, BN, FI, FJ, EPI, NT>(acc, yacc, smem, sc, t, lane, wm, wn, m0, n0, M, N, as, ws, bias, (half_t*)Cout, R, G, L);
     }
 }
 
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1, int WGM = 2>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1, int WGM = 2, int NW = 4>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                         const void* R, const void* G, int L, void* stream) {
     const size_t stage = (size_t)BM * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
@@ -671,10 +768,10 @@ static int launch_gemm8(const void* a, const void* w, const float* as, const flo
     size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
     if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
     if (lds > 160 * 1024 / MINB - (size_t)(BN * 4 + SC_BIAS(BN) + BM * 4)) return -1;
-    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB, WGM>;
+    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB, WGM, NW>;
     static std::atomic<size_t> configured[RDA_MAX_DEVICES];
     if (const int e = ensure_dynamic_lds((const void*)kern, lds, configured)) return e;
-    hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(GT), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
+    hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(64 * NW), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
                        (const half_t*)gs, (const half_t*)bias, c, M, N, K, (const half_t*)R, (const half_t*)G, L);
     return (int)hipGetLastError();
 }
@@ -712,7 +809,13 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
         // fragment to widen per k step instead of two (as 64 x 64), for two more A fragment reads from LDS.
         // The block's group scales are staged whole (BN x K / 128 halves), so past K = 3456 two blocks no longer fit a
         // CU's LDS: then one block per CU, which holds the scales of K up to ~45000.
-        if (group != 128 || K % 128 != 0 || N % 128 != 0) return -1;
+        if (group != 128 || K % 128 != 0 || N % 128 != 0 || !aligned(gs, 16)) return -1;
+        if (N % 256 == 0) {
+            const int e = launch_gemm8<128, 256, 128, 4, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            if (e >= 0) return e;
+            const int e3 = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            if (e3 >= 0) return e3;
+        }
         const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
         if (e >= 0) return e;
         return launch_gemm8<128, 128, 128, 3, W4, EPI, 1, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);

@@ -155,6 +155,12 @@ int rda_rms_norm_rope(const void* x, const float* w, void* y, int B, int H, int 
  * ticks and clocks[1] = 100 MHz real-time ticks over the run of workgroup 0's first wave. */
 int rda_calib_mfma_peak(int int8, int blocks, int iters, int* out, long long* clocks, void* stream);
 
+/* Measurement only, no counterpart in the reference: as rda_calib_mfma_peak, with each lane's operands taken from
+ * `operands` (16-byte aligned; blocks * 256 * 16 fragments of 16 bytes: lane l of workgroup b uses fragments
+ * (b * 256 + l) * 16 + 0..7 as A and + 8..15 as B, fp16 or int8 by `int8`), so the sustained rate on a given
+ * distribution of values (the matrix cores' power, and so the clock, depends on them) can be measured. */
+int rda_calib_mfma_peak_data(int int8, int blocks, int iters, const void* operands, int* out, long long* clocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -194,9 +194,11 @@ def test_swiglu_down_linear_bit_exact(dev, M, K, N):
     assert_same(bits(out), bits(ref))
 
 
-# K / 128 = 8, 4, 24 and 26 slices: whole and partial passes of the slice loop over the three stages; K = 12288 and 8192
-# (past K = 3456 the block's group scales no longer fit two blocks per CU: one block per CU)
-@pytest.mark.parametrize("M,N,K", [(520, 512, 1024), (300, 192, 512), (4096, 1024, 3072), (200, 256, 3328), (520, 256, 12288), (300, 384, 8192)])
+# K / 128 = 8, 4, 24 and 26 slices: whole and partial passes of the slice loop over the three stages; 2, 6 and 10 slices
+# (tail slices only; one pass and its tail); K = 12288 and 8192 (past K = 3456 the block's group scales no longer fit
+# two blocks per CU: one block per CU)
+@pytest.mark.parametrize("M,N,K", [(520, 512, 1024), (300, 192, 512), (4096, 1024, 3072), (200, 256, 3328), (520, 256, 12288), (300, 384, 8192),
+                                   (64, 128, 256), (200, 256, 768), (129, 128, 1280)])
 def test_w4a8_bit_exact(dev, M, N, K):
     print(f"w4a8 M={M} N={N} K={K}", flush=True)
     x = activations(M, K, seed=7, outliers=0)
