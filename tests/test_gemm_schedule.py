@@ -20,6 +20,12 @@ them. The model checks, for every wave pair at once:
 A schedule mistake (copying one slice later than the stages allow, a wait threshold one slice too loose, the
 barrier before the copies of the last k step dropped) fails one of these; test_model_catches_mistakes plants
 each of them.
+
+The W4A8 kernel (group-scaled, int4 weights, one W block per wave) runs a block-major slice of 16 products
+instead: the A fragment of product P is read after product P - 3 (the first three of slice 0 in the prologue,
+those of the next slice's first three after products 13-15), the next slice's packed W fragments after products 13
+and 14, the wait and barrier sit before product 13, and the copies of slice kt + NS go out after products 13-15.
+run_schedule_blockmajor models that order with the same checks.
 """
 import pytest
 
@@ -111,3 +117,89 @@ def test_model_catches_mistakes(NS, KS):
     assert run_schedule(NS, KS, KT, NI, copy_at=KS - 2)
     # the barrier before the last k step dropped
     assert run_schedule(NS, KS, KT, NI, barrier_last=False)
+
+
+class Model:
+    """Copies, waits, barriers and reads of the whole workgroup, with the race checks of run_schedule."""
+
+    def __init__(self, NS, KT, NI):
+        self.NS, self.KT, self.NI = NS, KT, NI
+        self.epoch = 0
+        self.inflight, self.landed, self.issued, self.holder, self.last_read, self.errors = [], {}, {}, {}, {}, []
+
+    def copy(self, s, n):
+        if not 0 <= s < self.KT:
+            self.errors.append(f"copy of missing slice {s}")
+            return
+        st = s % self.NS
+        prev = self.holder.get(st)
+        if prev is not None and prev != s and self.last_read.get(prev, -1) >= self.epoch:
+            self.errors.append(f"slice {s} copied into stage {st} in epoch {self.epoch} while slice {prev} is read there")
+        self.holder[st] = s
+        self.inflight += [s] * n
+        self.issued[s] = self.issued.get(s, 0) + n
+
+    def wait(self, keep):
+        while len(self.inflight) > keep:
+            s = self.inflight.pop(0)
+            if s not in self.inflight:
+                self.landed[s] = self.epoch
+
+    def barrier(self):
+        self.epoch += 1
+
+    def read(self, s):
+        if not 0 <= s < self.KT:
+            self.errors.append(f"read of missing slice {s}")
+            return
+        if self.landed.get(s, self.epoch) >= self.epoch or self.issued.get(s, 0) != self.NI:
+            self.errors.append(f"slice {s} read in epoch {self.epoch} before its copies landed")
+        if self.holder.get(s % self.NS) != s:
+            self.errors.append(f"slice {s} read from stage {s % self.NS}, which holds slice {self.holder.get(s % self.NS)}")
+        self.last_read[s] = self.epoch
+
+
+def run_schedule_blockmajor(NS, KT, NI=4, ahead_reads=3, barrier_at=13, copy_from=13, w_reads=(13, 14)):
+    m = Model(NS, KT, NI)
+    for s in range(min(NS, KT)):
+        m.copy(s, NI)
+    m.wait((NS - 1) * NI if KT >= NS else 0)
+    m.barrier()
+    m.read(0)  # the first products' A fragments and slice 0's packed W fragments
+    copy_at = sorted({copy_from + c * (16 - copy_from) // NI for c in range(NI)})
+    per = {p: sum(1 for c in range(NI) if copy_from + c * (16 - copy_from) // NI == p) for p in copy_at}
+    for kt in range(KT):
+        ahead, more = kt + NS < KT, kt + 1 < KT
+        for P in range(16):
+            if P == barrier_at:
+                m.wait((NS - 2) * NI if ahead else 0)
+                m.barrier()
+            n = P + ahead_reads  # the A fragment read after product P
+            if n < 16:
+                m.read(kt)
+            elif more:
+                m.read(kt + 1)
+            if more and P in w_reads:
+                m.read(kt + 1)
+            if ahead and P in per:
+                m.copy(kt + NS, per[P])
+    if set(m.last_read) != set(range(KT)):
+        m.errors.append("not every slice was read")
+    return m.errors
+
+
+@pytest.mark.parametrize("NS", [3, 4])
+@pytest.mark.parametrize("KT", list(range(1, 13)) + [24, 96])
+def test_blockmajor_schedule_is_race_free(NS, KT):
+    assert run_schedule_blockmajor(NS, KT) == []
+
+
+@pytest.mark.parametrize("NS", [3, 4])
+def test_blockmajor_model_catches_mistakes(NS):
+    KT = 10
+    # A fragments read only two products ahead: the read after product 13 is of this slice's stage, after the barrier
+    assert run_schedule_blockmajor(NS, KT, ahead_reads=2)
+    # the barrier one product later: the next slice's first A fragment is read before its copies are known to have landed
+    assert run_schedule_blockmajor(NS, KT, barrier_at=14)
+    # the copies of slice kt + NS issued before the barrier
+    assert run_schedule_blockmajor(NS, KT, copy_from=12)
