@@ -15,7 +15,9 @@ more than 512 MB of input copies so that the 256 MB Infinity Cache cannot serve 
 CPU baselines: every workload carries one -- the reference's own torch fallback for it (oracle/cpu_baseline.py: the
 dequantized matmul after a dense ConvRot for the linears, attention_bmm for attention, the fp32 cast RMSNorm, fp32
 decode attention, the unfused block), timed on the host cores on the same seeded inputs or a stated sample of them,
-with the host's CPU model, logical CPU count and torch thread count under "host".
+with the host's CPU model, logical CPU count and torch thread count under "host". Fallbacks that also run in the
+activations' dtype (attention and the linears) are timed in fp32 and in fp16; both rates are reported and the
+faster is the baseline's value.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME] [--cpu-only]
 
@@ -59,6 +61,10 @@ def parse():
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def dt_name(dt):
+    return {"torch.float32": "fp32", "torch.float16": "fp16"}[str(dt)]
 
 
 def gen(torch, seed):
@@ -485,25 +491,31 @@ def _cpu_w8a8(torch):
     return M, K, N, x, w, ws
 
 
-def c_attention(torch, heads=2):
+def c_attention(torch, heads=2, dtype=None):
     from oracle import cpu_baseline as cb
-    q, k, v = (t[:, :heads].float().contiguous() for t in attention_inputs(torch))
+    dt = dtype or torch.float32
+    q, k, v = (t[:, :heads].to(dt).contiguous() for t in attention_inputs(torch))
     return (lambda: cb.attention_bmm(q, k, v, 128 ** -0.5)), ATTN_FLOP * heads / 24, \
-        f"attention_bmm (attention.py:15-43) in fp32 over {heads} of the 24 heads, S=4096, D=128"
+        f"attention_bmm (attention.py:15-43) in {dt_name(dt)} over {heads} of the 24 heads, S=4096, D=128"
 
 
-def c_w8a8_gemm(torch):
+def c_w8a8_gemm(torch, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     M, K, N, x, w, ws = _cpu_w8a8(torch)
-    xr = cb.rotate(x, 128)
-    return (lambda: cb.linear_dequant(xr, w, ws)), 2.0 * M * N * K, "F.linear(x_rot, W.float() * ws) (int8_gemv.py:58-59), fp32, the full 4096x3072x3072"
+    xr = cb.rotate(x.to(dt), 128)
+    return (lambda: cb.linear_dequant(xr, w, ws)), 2.0 * M * N * K, \
+        f"F.linear(x_rot, W.to(dtype) * ws) (int8_gemv.py:58-59), {dt_name(dt)}, the full 4096x3072x3072"
 
 
-def c_w8a8_linear(torch):
+def c_w8a8_linear(torch, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     M, K, N, x, w, ws = _cpu_w8a8(torch)
-    H = cb.hadamard(128)
-    return (lambda: cb.w8a8_linear(x, w, ws, 128, H)), 2.0 * M * N * K, "dense group-128 ConvRot + F.linear(x_rot, W.float() * ws), fp32, full size"
+    H = cb.hadamard(128, dt)
+    x = x.to(dt)
+    return (lambda: cb.w8a8_linear(x, w, ws, 128, H)), 2.0 * M * N * K, \
+        f"dense group-128 ConvRot + F.linear(x_rot, W.to(dtype) * ws), {dt_name(dt)}, full size"
 
 
 def c_w8a8_rot_quant(torch):
@@ -513,26 +525,28 @@ def c_w8a8_rot_quant(torch):
     return (lambda: cb.rot_quant(x, 128, H)), M * K * 2 + M * K + M * 4, "dense group-128 ConvRot + per-token int8 quantization in torch, fp32, full size"
 
 
-def c_w4a8_gemm(torch):
+def c_w4a8_gemm(torch, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     M, K, N, x, _, _ = _cpu_w8a8(torch)
     N = 12288
     w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 8), dtype=torch.uint8)
     gs = (torch.rand(N, K // 128, generator=gen(torch, 9)) * 1.5e-2 + 5e-3).half()
-    xr = cb.rotate(x, 256)
+    xr = cb.rotate(x.to(dt), 256)
     return (lambda: cb.linear_w4_dequant(xr, w4, gs)), 2.0 * M * N * K, \
-        "int4 unpacked, group-128 scales applied, F.linear in fp32, the full 4096x12288x3072"
+        f"int4 unpacked, group-128 scales applied, F.linear in {dt_name(dt)}, the full 4096x12288x3072"
 
 
-def c_w4a8_gemm_k12288(torch):
+def c_w4a8_gemm_k12288(torch, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     M, K, N = 4096, 12288, 3072
-    x = torch.randn(M, K, generator=gen(torch, 23)).half().float()
+    x = torch.randn(M, K, generator=gen(torch, 23)).half().to(dt)
     w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 24), dtype=torch.uint8)
     gs = (torch.rand(N, K // 128, generator=gen(torch, 25)) * 1.5e-2 + 5e-3).half()
     xr = cb.rotate(x, 256)
     return (lambda: cb.linear_w4_dequant(xr, w4, gs)), 2.0 * M * N * K, \
-        "int4 unpacked, group-128 scales applied, F.linear in fp32, the full 4096x3072x12288"
+        f"int4 unpacked, group-128 scales applied, F.linear in {dt_name(dt)}, the full 4096x3072x12288"
 
 
 def c_mlp_rms_norm(torch):
@@ -553,23 +567,25 @@ def c_mlp_swiglu_rot_quant(torch):
         "F.silu(gate).mul_(up) in fp16, dense ConvRot (fp32), per-token int8, full 4096x8192"
 
 
-def c_mlp_down_gemm(torch):
+def c_mlp_down_gemm(torch, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     M, F, N = 4096, 8192, 3072
-    a = torch.randn(M, F, generator=gen(torch, 12))
+    a = torch.randn(M, F, generator=gen(torch, 12)).to(dt)
     w = torch.randint(-127, 128, (N, F), generator=gen(torch, 14), dtype=torch.int8)
     ws = (torch.rand(N, generator=gen(torch, 15)) * 2e-3 + 1e-3).float()
-    return (lambda: cb.linear_dequant(a, w, ws)), 2.0 * M * N * F, "F.linear(a, W.float() * ws), fp32, the full 4096x3072x8192"
+    return (lambda: cb.linear_dequant(a, w, ws)), 2.0 * M * N * F, f"F.linear(a, W.to(dtype) * ws), {dt_name(dt)}, the full 4096x3072x8192"
 
 
-def c_decode_gemv(torch, N):
+def c_decode_gemv(torch, N, dtype=None):
     from oracle import cpu_baseline as cb
+    dt = dtype or torch.float32
     K = 4096
-    x = torch.randn(1, K, generator=gen(torch, 16))
+    x = torch.randn(1, K, generator=gen(torch, 16)).to(dt)
     w = torch.randint(-127, 128, (N, K), generator=gen(torch, 17), dtype=torch.int8)
     s = (torch.rand(N, generator=gen(torch, 18)) * 2e-3 + 1e-3).float()
     return (lambda: cb.gemv(x, w, s)), N * K + N * 4 + K * 2 + N * 2, \
-        f"F.linear(x, W.float() * scale) (int8_gemv.py:58-59) for one fp32 token, K=4096, N={N}"
+        f"F.linear(x, W.to(dtype) * scale) (int8_gemv.py:58-59) for one {dt_name(dt)} token, K=4096, N={N}"
 
 
 def c_decode_attention(torch):
@@ -629,16 +645,36 @@ CPU_BASELINES = {
     "mlp_rms_norm": c_mlp_rms_norm,
     "mlp_swiglu_rot_quant": c_mlp_swiglu_rot_quant,
     "mlp_down_gemm": c_mlp_down_gemm,
-    "decode_gemv_n4096": lambda t: c_decode_gemv(t, 4096),
-    "decode_gemv_n1024": lambda t: c_decode_gemv(t, 1024),
-    "decode_gemv_n12288": lambda t: c_decode_gemv(t, 12288),
+    "decode_gemv_n4096": lambda t, **kw: c_decode_gemv(t, 4096, **kw),
+    "decode_gemv_n1024": lambda t, **kw: c_decode_gemv(t, 1024, **kw),
+    "decode_gemv_n12288": lambda t, **kw: c_decode_gemv(t, 12288, **kw),
     "decode_attention": c_decode_attention,
     "decode_layer": c_decode_layer,
     "dit_block": c_dit_block,
 }
 
 
+# Workloads whose reference fallback also runs in the activations' dtype (fp16): timed in fp32 and fp16, and the
+# faster is the baseline (both are reported). The others are fp32 by construction (the fp32 cast RMSNorm, the fp32
+# ConvRot before quantization, the fp32 decode cache, the unfused block in fp32).
+F16_BASELINES = ("attention_f16", "attention_i8qk", "w8a8_gemm", "w8a8_linear", "w4a8_gemm", "w4a8_gemm_k12288", "mlp_down_gemm",
+                 "decode_gemv_n4096", "decode_gemv_n1024", "decode_gemv_n12288")
+
+
 def cpu_baseline(torch, name, seconds=1.5, **kw):
+    """The CPU baseline of workload `name`: cpu_rate() in fp32 and, where the fallback also runs in fp16, in fp16; the
+    faster is `value` (SURVEY-style: label both, headline the faster)."""
+    rec = cpu_rate(torch, name, seconds, **kw)
+    rec["dtype"] = "fp32"
+    if name in F16_BASELINES:
+        r16 = cpu_rate(torch, name, seconds, dtype=torch.float16, **kw)
+        r16["dtype"] = "fp16"
+        fast, slow = (r16, rec) if r16["value"] > rec["value"] else (rec, r16)
+        rec = {**fast, "fp32": rec["value"], "fp16": r16["value"], "sample_" + slow["dtype"]: slow["sample"]}
+    return rec
+
+
+def cpu_rate(torch, name, seconds=1.5, **kw):
     """Times the CPU fallback of workload `name` on the host cores: calls back to back until `seconds` have passed (at
     least one); a first call shorter than a quarter of the budget is a discarded warm-up. Rate = work / mean time."""
     fn, work, sample = CPU_BASELINES[name](torch, **kw)
@@ -654,7 +690,7 @@ def cpu_baseline(torch, name, seconds=1.5, **kw):
     kind = PEAKS[WORKLOAD_BOUND[name]][0]
     rate = work / (elapsed / runs) / (1e12 if kind == "mfma" else 1e9)
     unit = "GB/s" if kind == "hbm" else "TOP/s" if WORKLOAD_BOUND[name] == "mfma_i8" else "TFLOP/s"
-    log(f"cpu {name}: {rate:.4g} {unit} ({runs} runs, {elapsed / runs * 1e3:.1f} ms each)")
+    log(f"cpu {name} {dt_name(kw.get('dtype') or torch.float32)}: {rate:.4g} {unit} ({runs} runs, {elapsed / runs * 1e3:.1f} ms each)")
     return {"value": round(rate, 5), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{sample}; {runs} timed runs, {elapsed / runs * 1e3:.2f} ms each"}
 
@@ -715,8 +751,8 @@ def main():
             if WORKLOAD_BOUND[name] in sustained:
                 rec["frac_of_random_operand_peak"] = round(rec["value"] / sustained[WORKLOAD_BOUND[name]], 4)
     if not args.no_cpu:
-        # The headline's sample is larger (6 of 24 heads, about 10 s); each component's is about 1.5 s.
-        result["cpu_baseline"] = cpu_baseline(torch, "attention_f16", seconds=10.0, heads=6)
+        # The headline's sample is larger (6 of 24 heads, about 6 s per dtype); each component's is about 1.5 s per dtype.
+        result["cpu_baseline"] = cpu_baseline(torch, "attention_f16", seconds=6.0, heads=6)
         result["host"] = host_info(torch)
         for name, rec in result.get("components", {}).items():
             rec["cpu_baseline"] = cpu_baseline(torch, name)

@@ -96,3 +96,19 @@ def test_block_chain_invariants():
 
 def test_cpu_model_string():
     assert isinstance(cb.cpu_model(), str) and cb.cpu_model()
+
+
+def test_fp16_legs_compute_the_same_functions():
+    """bench.py also times the linears and attention_bmm with fp16 inputs: the same functions, within fp16 rounding."""
+    x = torch.randn(5, 256, generator=g)
+    w = torch.randint(-127, 128, (64, 256), generator=g, dtype=torch.int8)
+    s = torch.rand(64, generator=g) * 2e-3 + 1e-3
+    ref = f64(x.half()) @ (f64(w) * f64(s)[:, None]).T
+    out = cb.linear_dequant(x.half(), w, s)
+    assert out.dtype == torch.float16
+    assert np.abs(f64(out) - ref).max() <= 2e-3 * np.abs(ref).max()
+    q, k, v = (torch.randn(1, 2, 64, 128, generator=g).half() for _ in range(3))
+    out = cb.attention_bmm(q, k, v, 128 ** -0.5)
+    assert out.dtype == torch.float16
+    ref = oracle.attention_f64(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5)
+    assert np.abs(f64(out) - ref).max() < 5e-3
