@@ -5,7 +5,8 @@
 // Arithmetic follows attn / attn_i8 (hip_attention.hip:160-373): scores s in fp32; the running
 // maximum m only moves when some row's block maximum exceeds m + 8 (the lazy rescale,
 // hip_attention.hip:333-340; applied to the whole wave when any of its rows needs it); p =
-// exp2(s * scale_log2 - m) (int8: exp2(s - m) with s already scaled); P is rounded to fp16
+// exp2(s * scale_log2 - m) (int8: s = the int32 score times the key's scale, and the row factor q_scale *
+// scale_log2 multiplies it in the same FMA); P is rounded to fp16
 // before PV and l sums those fp16 values (in fp32, by v_dot2 with ones, which halves the adds;
 // the reference sums the fp32 p); out = fp16(o * (1 / l)). The block maximum is only computed
 // when a tile's P, made first with the current m, shows that a row may need the rescale (see
@@ -285,25 +286,28 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
                 hook(ks);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            // Scores times the per-key scales only; the per-row factor (Q's scale times scale log2 e) enters the exponent's
+            // FMA (exps) and the slow path's maximum.
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++) {
                 const f4 sc = *(const f4*)(smem + st_u + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
 #pragma unroll
-                for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * score_scale * sc[e];  // hip_attention.hip:227
+                for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * sc[e];  // hip_attention.hip:227
             }
         }
     };
     auto no_hook = [](int) {};
-    // Keys past Lk (hip_attention.hip:324-328): only the last tile can reach past Lk.
+    // Keys past Lk (hip_attention.hip:324-328): only the last tile can reach past Lk. int8: -inf, since its scores are
+    // scaled only in the exponent, by a factor that an all-zero Q row takes down to 1e-30 x scale log2 e.
     auto mask = [&](float (&x)[16], int key0) __attribute__((always_inline)) {
         if (key0 + KB > p.Lk) {
 #pragma unroll
             for (int r = 0; r < 16; r++)
-                if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) x[r] = -1e30f;
+                if (key0 + 8 * (r >> 2) + 4 * g + (r & 3) >= p.Lk) x[r] = I8 ? -__builtin_inff() : -1e30f;
         }
     };
 
-    // The online softmax of a tile with scores s: P = exp2(s * scale_log2 - m) (int8: exp2(s - m)), rounded to fp16 into
+    // The online softmax of a tile with scores s: P = exp2(s * scale_log2 - m) (int8: exp2(s * score_scale - m)), rounded to fp16 into
     // pf, and l += the fp16 P (in fp32, by v_dot2 with ones). `exps(k)` does the k-th of eight (int8: four) equal parts.
     float s[16];
     h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
@@ -311,8 +315,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     auto exps = [&](int k) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = k * PER; r < (k + 1) * PER; r += 2) {
-            const float e0 = I8 ? __builtin_amdgcn_exp2f(s[r] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], p.scale_log2, -m));
-            const float e1 = I8 ? __builtin_amdgcn_exp2f(s[r + 1] - m) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], p.scale_log2, -m));
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], I8 ? score_scale : p.scale_log2, -m));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], I8 ? score_scale : p.scale_log2, -m));
             const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
             l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);  // l sums the fp16 P of PV
             pf[r >> 3][r & 7] = pk[0];
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             for (int r = 1; r < 16; r++) mx = fmaxf(mx, s[r]);
             const f2 mh = halves(mx);
             mx = fmaxf(mh[0], mh[1]);
-            if (!I8) mx *= p.scale_log2;
+            mx *= I8 ? score_scale : p.scale_log2;
             l = l_old;
             if (__any(mx > m + 8.f)) {
                 const float mn = fmaxf(m, mx), alpha = __builtin_amdgcn_exp2f(m - mn);

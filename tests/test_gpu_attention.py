@@ -48,6 +48,21 @@ def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
     close(out, ref)
 
 
+@pytest.mark.parametrize("int8_qk", [False, True])
+def test_attention_zero_query_rows(dev, int8_qk):
+    """All-zero query rows (the int8 row scale then sits at its 1e-30 floor) with a partial last key tile: the keys past
+    Lk must get no weight, so each such row is the mean of the valid V rows."""
+    print(f"attention zero query rows int8_qk={int8_qk}", flush=True)
+    q, k, v = qkv(1, 2, 2, 70, 150, seed=8)
+    q[:, :, ::3] = 0
+    out = torch.empty(1, 2, 70, 128, dtype=torch.float16, device=dev)
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5, int8_qk)
+    ref = (oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64)(q.numpy(), k.numpy(), v.numpy(), 128 ** -0.5)
+    close(out, ref)
+    mean = v.double().numpy().mean(axis=2)  # (B, H, 128)
+    assert np.abs(out[:, :, ::3].cpu().double().numpy() - mean[:, :, None]).max() <= 2e-3
+
+
 def test_attention_matches_reference_loop(dev):
     """Tighter: the reference's own loop restated in fp32 (lazy rescale, fp16 P) agrees with the kernel."""
     q, k, v = qkv(1, 2, 2, 256, 700, seed=3)
