@@ -203,3 +203,31 @@ def test_blockmajor_model_catches_mistakes(NS):
     assert run_schedule_blockmajor(NS, KT, barrier_at=14)
     # the copies of slice kt + NS issued before the barrier
     assert run_schedule_blockmajor(NS, KT, copy_from=12)
+
+
+def tile_of(block, gx, gy, strips):
+    """gemm8_kernel's block remap: block id -> (bx, by). Ids go round-robin to the 8 XCDs; XCD x takes the
+    (gy / 2) x (gx / 4) sub-grid x, row by row, or (strips: the eight-wave W4A8 kernel) in strips four tiles tall,
+    column by column."""
+    by, bx = divmod(block, gx)
+    if gx % 4 or gy % 2:
+        return bx, by
+    x, r, sx, sy = block % 8, block // 8, gx // 4, gy // 2
+    if strips and sy % 4 == 0:
+        strip, w = divmod(r, 4 * sx)
+        return (x % 4) * sx + w // 4, (x // 4) * sy + strip * 4 + w % 4
+    return (x % 4) * sx + r % sx, (x // 4) * sy + r // sx
+
+
+@pytest.mark.parametrize("strips", [False, True])
+@pytest.mark.parametrize("gx,gy", [(48, 32), (12, 16), (16, 16), (4, 8), (8, 4), (96, 32), (6, 3), (5, 8)])
+def test_tile_order_is_a_permutation(gx, gy, strips):
+    tiles = [tile_of(b, gx, gy, strips) for b in range(gx * gy)]
+    assert sorted(tiles) == sorted((x, y) for x in range(gx) for y in range(gy))
+
+
+def test_strip_order_groups_square_blocks():
+    """With one block per CU (32 per XCD at a time), the first 32 tiles of an XCD span 4 rows x 8 columns."""
+    gx, gy = 48, 32
+    first = [tile_of(b, gx, gy, True) for b in range(0, 8 * 32, 8)]  # XCD 0's first 32 blocks
+    assert len({y for _, y in first}) == 4 and len({x for x, _ in first}) == 8
