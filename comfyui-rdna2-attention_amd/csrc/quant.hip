@@ -92,6 +92,13 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// (int)floorf(x) in one instruction (the compiler emits a floor and a truncation); x is finite here.
+__device__ __forceinline__ int cvt_floor(float x) {
+    int r;
+    asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
+
 __device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
     return (u32)(a & 255) | ((u32)(b & 255) << 8) | ((u32)(c & 255) << 16) | ((u32)(d & 255) << 24);
 }
@@ -271,11 +278,13 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                             v[b + i + 4] = p - q;
                         }
                 }
+                // The row maximum is taken before the rounding to fp16 and rounded once at the end: rounding is monotonic,
+                // so max(round |p|) = round(max |p|), one conversion per element fewer.
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const half_t y = to_half(v[i] * norm);
-                    rotated[g * GROUP + e[i]] = y;
-                    mx = fmaxf(mx, fabsf((float)y));
+                    const float y = v[i] * norm;
+                    rotated[g * GROUP + e[i]] = to_half(y);
+                    mx = fmaxf(mx, fabsf(y));
                 }
             }
             wave_sync();
@@ -288,6 +297,7 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
     mx = red[0];
 #pragma unroll
     for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
+    if (GROUP != 0) mx = r16(mx);  // the largest |rotated fp16 value| (see the rotation pass)
     const float scale = I4 ? fmaxf(mx, 1e-10f) / 7.f : fmaxf(mx / 127.f, 1e-30f);
     if (t == 0) as[row] = scale;
 
@@ -301,8 +311,10 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
         for (int i = 0; i < 16; i++) {
             const float f = (float)(i < 8 ? lo[i] : hi[i - 8]);
             const float d = div_by_scale(f, scale, rcp);  // f / scale
-            if (I4) q[i] = (int)fminf(fmaxf(rintf(d), -7.f), 7.f);  // int8_gemm.hip:84
-            else q[i] = (int)fminf(fmaxf(floorf(d + 0.5f), -128.f), 127.f);  // int8_gemm.hip:53
+            // int8_gemm.hip:84 and :53. The clamp to [lo, hi] (integers) goes before the rounding: both orders give the same
+            // code for every input, NaN included (-128 / -7), and floor then truncation fuse into one conversion.
+            if (I4) q[i] = (int)rintf(fminf(fmaxf(d, -7.f), 7.f));
+            else q[i] = cvt_floor(fminf(fmaxf(d + 0.5f, -128.f), 127.f));
         }
         u4v o;
 #pragma unroll
