@@ -569,7 +569,9 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm8_kernel(const int8_t* __re
         if (PIPE) break;
         fr[0][f] = W4 && f >= FI ? widen(wraw(stage(0), 0, f - FI)) : frag(stage(0), 0, f);
     }
-    // PIPE (below): the first three products' A fragments, slice 0's packed W fragments, the first one widened.
+    // PIPE (below): the first three products' A fragments, slice 0's packed W fragments, the first one widened. (These
+    // arrays have one element in the other instantiations, which never use them; indices there are written `PIPE ? i : 0`
+    // so that those instantiations compile without out-of-range constants.)
     i4v afr[PIPE ? 4 : 1], wf[PIPE ? 4 : 1];
     u2v wr[PIPE ? 4 : 1];
     h4v gva[PIPE ? 4 : 1][4];  // [0]: scales of the slice's blocks 0, 1 fold; [1]: of its blocks 2, 3 (folded in the next slice)
