@@ -207,13 +207,13 @@ def test_blockmajor_model_catches_mistakes(NS):
 
 def tile_of(block, gx, gy, strips):
     """gemm8_kernel's block remap: block id -> (bx, by). Ids go round-robin to the 8 XCDs; XCD x takes the
-    (gy / 2) x (gx / 4) sub-grid x, row by row, or (strips: the eight-wave W4A8 kernel) in strips four tiles tall,
-    column by column."""
+    (gy / 2) x (gx / 4) sub-grid x, row by row, or (strips: the eight-wave W4A8 kernel, sub-grids at least 8 tiles wide)
+    in strips four tiles tall, column by column."""
     by, bx = divmod(block, gx)
     if gx % 4 or gy % 2:
         return bx, by
     x, r, sx, sy = block % 8, block // 8, gx // 4, gy // 2
-    if strips and sy % 4 == 0:
+    if strips and sy % 4 == 0 and sx >= 8:
         strip, w = divmod(r, 4 * sx)
         return (x % 4) * sx + w // 4, (x // 4) * sy + strip * 4 + w % 4
     return (x % 4) * sx + r % sx, (x // 4) * sy + r // sx
