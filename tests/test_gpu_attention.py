@@ -112,21 +112,25 @@ def test_comfy_backend_strided_layout(dev):
     close(out8.reshape(B, L, H, 128).transpose(1, 2), oracle.attention_i8qk_f64(th(q), th(k), th(v), 128 ** -0.5))
 
 
-def test_pack_k_i8_bit_exact(dev):
-    B, Hkv, Lk = 1, 2, 100
+@pytest.mark.parametrize("B,Hkv,Lk", [(1, 2, 100), (2, 3, 33), (1, 1, 64), (1, 2, 70), (1, 1, 4101)])
+def test_pack_k_i8_bit_exact(dev, B, Hkv, Lk):
+    """Every key's codes and scale against the oracle; rows past Lk, up to the padded length (a multiple of the 32-key
+    tile), are zero. Lk values end the 64-key workgroups at each kind of boundary."""
+    print(f"pack_k_i8 B={B} Hkv={Hkv} Lk={Lk}", flush=True)
     _, k, _ = qkv(B, Hkv, Hkv, 1, Lk, seed=4)
     lib = _lib.load()
     ws = torch.empty(lib.rda_attn_i8_workspace(B, Hkv, Lk), dtype=torch.uint8, device=dev)
     kd = k.to(dev)
     _lib.check(lib.rda_pack_k_i8(_lib.ptr(kd), _lib.ptr(ws), B, Hkv, Lk, *kd.stride()[:3], _lib.stream()))
-    pad = (Lk + 63) // 64 * 64
+    pad = (Lk + 31) // 32 * 32
+    assert ws.numel() == B * Hkv * pad * (128 + 4)
     k8 = ws[:B * Hkv * pad * 128].view(torch.int8).view(B * Hkv, pad, 128).cpu().numpy()
     ks = ws[B * Hkv * pad * 128:].view(torch.float32).view(B * Hkv, pad).cpu().numpy()
-    for h in range(Hkv):
-        q_ref, s_ref = oracle.quant_rows_rint(k[0, h].numpy())
-        assert_same(k8[h, :Lk], q_ref)
-        assert_same(ks[h, :Lk], s_ref)
-        assert not k8[h, Lk:].any()
+    for bh in range(B * Hkv):
+        q_ref, s_ref = oracle.quant_rows_rint(k[bh // Hkv, bh % Hkv].numpy())
+        assert_same(k8[bh, :Lk], q_ref)
+        assert_same(ks[bh, :Lk], s_ref)
+        assert not k8[bh, Lk:].any()
 
 
 def test_attention_full_size_sampled(dev):
