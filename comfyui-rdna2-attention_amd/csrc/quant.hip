@@ -81,9 +81,13 @@ __device__ __forceinline__ bool silu_sure_tiny(float q) {
 // finite fp16 gate through the kernel.
 __device__ __forceinline__ float sigmoid_exact(float g) { return 1.f / (1.f + rda_expf(-g)); }
 __device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
-// int8_gemm.hip:140-143
-__device__ __forceinline__ float modulate(float x, float rstd, float w, float s, float t) {
-    return r16(r16(r16(x * rstd * (w + 1.f)) * s) + t);
+// The kernels round "r16(a * b)" and "r16(a + b)" of two fp16 values in pairs, as fp16 products and sums (v_pk_mul_f16,
+// v_pk_add_f16): the fp32 product of two fp16 values is exact, so rounding it to fp16 gives the fp16 product; an fp32
+// sum rounded again to fp16 is the correctly rounded fp16 sum too (a second rounding is harmless when the first keeps
+// at least 2 x 11 + 2 significant bits, as fp32's 24 do). -ffp-contract=off keeps "a * s + t" two roundings.
+__device__ __forceinline__ h2 to_half2(float a, float b) {
+    asm("" : "+v"(a), "+v"(b));  // round to fp32 first, as in to_half
+    return __builtin_convertvector((f2){a, b}, h2);
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -201,7 +205,11 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                         }
                     }
 #pragma unroll
-                    for (int i = 0; i < 16; i++) v[i] = r16(r16(sg[i]) * (float)(i < 8 ? ulo[i] : uhi[i - 8]));
+                    for (int i = 0; i < 16; i += 2) {
+                        const h2 pr = to_half2(sg[i], sg[i + 1]) * (h2){i < 8 ? ulo[i] : uhi[i - 8], i < 8 ? ulo[i + 1] : uhi[i - 7]};
+                        v[i] = (float)pr[0];
+                        v[i + 1] = (float)pr[1];
+                    }
                 } else if (ACT == GATE) {
                     const half_t* u = U + (size_t)row * K;
                     const h8 ulo = *(const h8*)(u + e0), uhi = *(const h8*)(u + e0 + 8);
@@ -223,7 +231,11 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                         }
                     }
 #pragma unroll
-                    for (int i = 0; i < 16; i++) v[i] = r16((float)(i < 8 ? lo[i] : hi[i - 8]) * r16(sg[i]));
+                    for (int i = 0; i < 16; i += 2) {
+                        const h2 pr = (h2){i < 8 ? lo[i] : hi[i - 8], i < 8 ? lo[i + 1] : hi[i - 7]} * to_half2(sg[i], sg[i + 1]);
+                        v[i] = (float)pr[0];
+                        v[i + 1] = (float)pr[1];
+                    }
                 } else if (ACT == MOD) {
                     const h8 slo = *(const h8*)(ms + e0), shi = *(const h8*)(ms + e0 + 8);
                     const h8 tlo = *(const h8*)(mt + e0), thi = *(const h8*)(mt + e0 + 8);
@@ -231,9 +243,14 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                     const f4 w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
                     const float wv[16] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w, w3.x, w3.y, w3.z, w3.w};
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        v[i] = modulate((float)lo[i], rstd, wv[i], (float)slo[i], (float)tlo[i]);
-                        v[8 + i] = modulate((float)hi[i], rstd, wv[8 + i], (float)shi[i], (float)thi[i]);
+                    for (int i = 0; i < 16; i += 2) {
+                        // modulate (int8_gemm.hip:140-143): r16(r16(r16(x rstd (w + 1)) s) + t), two elements at a time.
+                        const h8 &xs = i < 8 ? lo : hi, &ss = i < 8 ? slo : shi, &ts = i < 8 ? tlo : thi;
+                        const int j = i & 7;
+                        const h2 a = to_half2((float)xs[j] * rstd * (wv[i] + 1.f), (float)xs[j + 1] * rstd * (wv[i + 1] + 1.f));
+                        const h2 m = a * (h2){ss[j], ss[j + 1]} + (h2){ts[j], ts[j + 1]};
+                        v[i] = (float)m[0];
+                        v[i + 1] = (float)m[1];
                     }
                 } else {
 #pragma unroll
