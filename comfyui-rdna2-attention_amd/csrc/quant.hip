@@ -51,36 +51,6 @@ __device__ __forceinline__ float situ(float hidden, float gate) {
     const float sigmoid = 1.f / (1.f + rda_exp2f(-1.442695041f * gate));
     return r16(4.f * soft_tanh(gate * 0.25f) * sigmoid * 25.f * soft_tanh(hidden * 0.04f));
 }
-// SwiGLU (int8_gemm.hip:130-132): r16(r16(silu(g)) u) with silu(g) = g / (1 + rda_expf(-g)) in fp32.
-// silu by a fast path: hardware exp2 of a rounded argument and a hardware reciprocal. Over every fp16 g whose
-// silu is an fp16 normal number the fast value is within 11 fp32 ulps of the exact one (measured on all 65536
-// inputs: <= 4 ulps for |g| < 4), so where it lies more than SILU_T ulps from an fp16 rounding midpoint both
-// round to the same fp16 value. Below 2^-14 (g < about -12) the results fall on fp16's subnormal grid, whose
-// spacing 2^-24 continues that of the lowest normal binade: there the test is the distance of |q| 2^24 from
-// the nearest half-integer, again against SILU_T ulps (silu_sure_tiny; the fast value's error stays within the
-// same bound there, and the tiny values that round to zero are sure by the same test). Values that pass neither
-// (about 0.3% of inputs, and results from 2^15 up or not finite) take the exact formula; the SwiGLU tests
-// compare all 65536 fp16 gates with the oracle through the kernel.
-#define SILU_T 12
-__device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
-__device__ __forceinline__ bool silu_sure(float q) {
-    // The 13 bits below the fp16 mantissa within SILU_T of the midpoint 0x1000, by one add and mask.
-    const bool mid = ((__float_as_uint(q) + (SILU_T - 0x1000)) & 0x1fffu) <= 2 * SILU_T;
-    const float a = fabsf(q);
-    return !mid && a >= __uint_as_float(0x38800040u) && a < 32768.f;
-}
-__device__ __forceinline__ bool silu_sure_tiny(float q) {
-    const float r = fabsf(q) * 16777216.f;  // exact: |q| in units of the fp16 grid spacing 2^-24
-    const float f = r - floorf(r);          // exact
-    const float ulp = __uint_as_float(__float_as_uint(r) & 0x7f800000u) * (1.f / 8388608.f);
-    return r < 1024.f && fabsf(f - 0.5f) > SILU_T * ulp;
-}
-// int8_gemm.hip:135-137: r16(x r16(sigmoid(gate))), sigmoid(g) = 1 / (1 + rda_expf(-g)) in fp32. The kernel takes
-// sigmoid from the same kind of fast path as silu (hardware exp2 and reciprocal) where the result is sure to round
-// to the same fp16 value (silu_sure, silu_sure_tiny), and this exact formula elsewhere; the gate tests run every
-// finite fp16 gate through the kernel.
-__device__ __forceinline__ float sigmoid_exact(float g) { return 1.f / (1.f + rda_expf(-g)); }
-__device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
 // The kernels round "r16(a * b)" and "r16(a + b)" of two fp16 values in pairs, as fp16 products and sums (v_pk_mul_f16,
 // v_pk_add_f16): the fp32 product of two fp16 values is exact, so rounding it to fp16 gives the fp16 product; an fp32
 // sum rounded again to fp16 is the correctly rounded fp16 sum too (a second rounding is harmless when the first keeps
@@ -88,6 +58,36 @@ __device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn
 __device__ __forceinline__ h2 to_half2(float a, float b) {
     asm("" : "+v"(a), "+v"(b));  // round to fp32 first, as in to_half
     return __builtin_convertvector((f2){a, b}, h2);
+}
+// SwiGLU (int8_gemm.hip:130-132): r16(r16(silu(g)) u) with silu(g) = g / (1 + rda_expf(-g)) in fp32; the sigmoid
+// gate (int8_gemm.hip:135-137): r16(x r16(sigmoid(gate))), sigmoid(g) = 1 / (1 + rda_expf(-g)) in fp32.
+// Both take a fast path -- hardware exp2 of a rounded argument and a hardware reciprocal -- whose value q lies
+// within 11 fp32 ulps of the exact one over every fp16 input (measured on all 65536; <= 4 ulps for |g| < 4).
+// round_sure rounds the two ends of [q (1 - d), q (1 + d)], d = 13 x 2^-23 (at least 12 ulps of q on either side
+// after the ends' own fp32 rounding), to fp16: where both give the same fp16 value, every value between them rounds
+// to it as well, the exact one included, and that is r16 of the exact value. This holds on fp16's subnormal grid
+// and at the overflow threshold too, and values too small for fp32's normal range round to zero either way. The
+// pairs where the ends differ (about 0.3% of values) take the exact formula; the SwiGLU and gate tests run every
+// finite fp16 gate through the kernels and compare the codes, which then fix r16 of the value, with the oracle's.
+__device__ __forceinline__ float silu_fast(float g) { return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
+__device__ __forceinline__ float silu_exact(float g) { return g / (1.f + rda_expf(-g)); }
+__device__ __forceinline__ float sigmoid_fast(float g) { return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f)); }
+__device__ __forceinline__ float sigmoid_exact(float g) { return 1.f / (1.f + rda_expf(-g)); }
+template <class Exact>
+__device__ __forceinline__ h2 round_sure(float q0, float q1, Exact exact) {
+    constexpr float lo_f = 1.f - 0x1.ap-20f, hi_f = 1.f + 0x1.ap-20f;  // 1 -+ 13 x 2^-23, both exact in fp32
+    const h2 lo = to_half2(q0 * lo_f, q1 * lo_f), hi = to_half2(q0 * hi_f, q1 * hi_f);
+    const u32 diff = __builtin_bit_cast(u32, lo) ^ __builtin_bit_cast(u32, hi);
+    const bool unsure0 = (diff & 0xffffu) != 0, unsure1 = (diff >> 16) != 0;
+    h2 r = lo;
+    // Element by element, so that a wave runs the exact formula only for the elements some lane needs it for.
+    if (__any(unsure0)) {
+        if (unsure0) r[0] = to_half(exact(0));
+    }
+    if (__any(unsure1)) {
+        if (unsure1) r[1] = to_half(exact(1));
+    }
+    return r;
 }
 
 __device__ __forceinline__ void wave_sync() {
@@ -184,55 +184,22 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                 } else if (ACT == SWIGLU) {
                     const half_t* u = U + (size_t)row * K;
                     const h8 ulo = *(const h8*)(u + e0), uhi = *(const h8*)(u + e0 + 8);
-                    float sg[16];
-                    bool unsure[16];
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        sg[i] = silu_fast((float)(i < 8 ? lo[i] : hi[i - 8]));
-                        unsure[i] = !silu_sure(sg[i]);
-                    }
-                    // For the positions where some lane of the wave is unsure: the subnormal-range test, then the exact
-                    // formula where that does not settle it either.
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        if (__any(unsure[i])) {
-                            unsure[i] = unsure[i] && !silu_sure_tiny(sg[i]);
-                            if (__any(unsure[i])) {
-                                const float gi = (float)(i < 8 ? lo[i] : hi[i - 8]);
-                                const float exact = gi / (1.f + rda_expf(-gi));
-                                if (unsure[i]) sg[i] = exact;
-                            }
-                        }
-                    }
 #pragma unroll
                     for (int i = 0; i < 16; i += 2) {
-                        const h2 pr = to_half2(sg[i], sg[i + 1]) * (h2){i < 8 ? ulo[i] : uhi[i - 8], i < 8 ? ulo[i + 1] : uhi[i - 7]};
+                        const float g0 = (float)(i < 8 ? lo[i] : hi[i - 8]), g1 = (float)(i < 8 ? lo[i + 1] : hi[i - 7]);
+                        const h2 sg = round_sure(silu_fast(g0), silu_fast(g1), [&](int k) { return silu_exact(k ? g1 : g0); });
+                        const h2 pr = sg * (h2){i < 8 ? ulo[i] : uhi[i - 8], i < 8 ? ulo[i + 1] : uhi[i - 7]};
                         v[i] = (float)pr[0];
                         v[i + 1] = (float)pr[1];
                     }
                 } else if (ACT == GATE) {
                     const half_t* u = U + (size_t)row * K;
                     const h8 ulo = *(const h8*)(u + e0), uhi = *(const h8*)(u + e0 + 8);
-                    float sg[16];
-                    bool unsure[16];
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        sg[i] = sigmoid_fast((float)(i < 8 ? ulo[i] : uhi[i - 8]));
-                        unsure[i] = !silu_sure(sg[i]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        if (__any(unsure[i])) {
-                            unsure[i] = unsure[i] && !silu_sure_tiny(sg[i]);
-                            if (__any(unsure[i])) {
-                                const float exact = sigmoid_exact((float)(i < 8 ? ulo[i] : uhi[i - 8]));
-                                if (unsure[i]) sg[i] = exact;
-                            }
-                        }
-                    }
 #pragma unroll
                     for (int i = 0; i < 16; i += 2) {
-                        const h2 pr = (h2){i < 8 ? lo[i] : hi[i - 8], i < 8 ? lo[i + 1] : hi[i - 7]} * to_half2(sg[i], sg[i + 1]);
+                        const float g0 = (float)(i < 8 ? ulo[i] : uhi[i - 8]), g1 = (float)(i < 8 ? ulo[i + 1] : uhi[i - 7]);
+                        const h2 sg = round_sure(sigmoid_fast(g0), sigmoid_fast(g1), [&](int k) { return sigmoid_exact(k ? g1 : g0); });
+                        const h2 pr = (h2){i < 8 ? lo[i] : hi[i - 8], i < 8 ? lo[i + 1] : hi[i - 7]} * sg;
                         v[i] = (float)pr[0];
                         v[i + 1] = (float)pr[1];
                     }
