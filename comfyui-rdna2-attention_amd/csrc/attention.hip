@@ -12,16 +12,18 @@
 // when a tile's P, made first with the current m, shows that a row may need the rescale (see
 // settle below): the outcome is the same as computing it for every tile.
 //
-// Work split. A workgroup of four wave64s owns 128 query rows of one (batch, head) and walks the
-// whole key range; each wave owns 32 query rows and keeps Q, O, l and m for them in registers
-// (<= 168 VGPRs). Three workgroups share a CU (three waves per SIMD, 3 x 16 KiB of LDS each), so
-// the attention configuration (24 heads x 4096 rows = 768 workgroups) runs in one round, and
-// while one workgroup waits at its barrier or for LDS, the others keep the matrix cores busy
-// (one eight-wave workgroup per CU, with two waves per SIMD in lockstep between barriers, left
-// the matrix cores idle for half the cycles). Block ids are remapped so that the workgroups an
-// XCD runs together belong to one head and share its K/V through that XCD's L2.
+// Work split. Each wave owns 32 query rows and walks the whole key range, keeping Q, O, l and m for
+// its rows in registers (<= 168 VGPRs, three waves per SIMD). When every head has a multiple of 32
+// query rows and at least 384, a workgroup is twelve waves over 384 consecutive rows of the rows
+// flattened over (batch, head, row), one workgroup per CU: the attention configuration (24 heads x
+// 4096 rows) is 256 workgroups, one round, and each K/V tile is copied once for twelve waves rather
+// than once per four (copies measured at ~8% of the kernel). A workgroup's rows then lie in one head
+// or two; with two it keeps a second set of tiles, copied by waves 8-11 (waves 0-7 copy the first),
+// and each wave reads the set of its own head. Otherwise a workgroup is four waves over 128 rows of
+// one head, three to a CU. Block ids are remapped so that the workgroups an XCD runs together cover
+// a contiguous range of heads and share their K/V through that XCD's L2.
 //
-// Tiles. Each workgroup keeps 32-key tiles of K and V in three LDS stages. They are copied by
+// Tiles. Each workgroup keeps 32-key tiles of K and V (one or two sets) in three LDS stages. They are copied by
 // direct global->LDS loads (global_load_lds_dwordx4: lane i of a wave writes the 16 bytes at LDS
 // base + 16 i), issued one step ahead, so no register holds a tile in flight and the load
 // latency hides behind a full step of work; the s_waitcnt before each step's closing barrier is
@@ -44,9 +46,9 @@
 // i % 4 of the 8-byte read of lane 4 e + i / 4 as its element e.
 #include "common.h"
 
-#define AT 256  // threads per workgroup: four waves
-#define QB 128  // query rows per workgroup (32 per wave)
-#define KB 32   // keys per tile
+#define QB 128         // query rows of a four-wave workgroup (32 per wave)
+#define FLAT_ROWS 384  // query rows of a twelve-wave workgroup
+#define KB 32          // keys per tile
 
 struct AttnArgs {
     const half_t* q;
@@ -56,6 +58,7 @@ struct AttnArgs {
     const int8_t* k8;  // int8 K [B * Hkv][Lk_pad][128]
     const float* ks;   // per-key scales [B * Hkv][Lk_pad]
     int H, Hkv, Lq, Lk, Lk_pad, qblocks, nblocks;
+    long rows;  // B H Lq, the query rows flattened over (batch, head, row)
     long sqb, sqh, sql, skb, skh, skl, svb, svh, svl, sob, soh, sol;
     float scale_log2;
 };
@@ -66,9 +69,11 @@ struct Tile {
     static constexpr int SC_BYTES = I8 ? 256 : 0;  // int8 per-key scales: one 256-byte copy, KB floats used
     static constexpr int K_BYTES = KB * K_ROW + SC_BYTES;
     static constexpr int V_BYTES = KB * 256;
-    static constexpr int BYTES = K_BYTES + V_BYTES;  // one stage: K, then V
-    static constexpr int LDS = 3 * BYTES;  // three stages
+    static constexpr int BYTES = K_BYTES + V_BYTES;  // one tile: K, then V
 };
+// Three stages, each of one tile (four waves) or of two, one per head among the workgroup's rows (twelve waves).
+template <bool I8, int NWV>
+constexpr int attn_lds() { return 3 * (NWV == 12 ? 2 : 1) * Tile<I8>::BYTES; }
 
 typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4_t;
@@ -91,10 +96,11 @@ template <int N>
 __device__ __forceinline__ constexpr std::integral_constant<int, (N + 1) % 3> next_stage(std::integral_constant<int, N>) { return {}; }
 __device__ __forceinline__ int next_stage(int s) { return s == 2 ? 0 : s + 1; }
 
-template <bool I8>
-__global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_kernel(AttnArgs p) {
+template <bool I8, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_kernel(AttnArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     using T = Tile<I8>;
+    constexpr int SS = (NWV == 12 ? 2 : 1) * T::BYTES;  // bytes per stage
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, lq = lane & 31;
     const int wq = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar
 
@@ -102,9 +108,34 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // of (head, q-block) work so its resident workgroups share K/V through its L2.
     int blk = blockIdx.x;
     if (p.nblocks % 8 == 0) blk = (blk % 8) * (p.nblocks / 8) + blk / 8;
-    const int bh = blk / p.qblocks, qblk = blk % p.qblocks;
-    const int b = bh / p.H, h = bh % p.H, hk = h / (p.H / p.Hkv);
-    const int q0 = qblk * QB + wq * 32;
+    // The wave's query rows q0 .. q0 + 31 of head h of batch b. Tile set c of the workgroup holds the K/V of batch
+    // kvb[c], KV head kvh[c]; the wave reads set `set`. Four waves: one set, 128 rows of one head. Twelve waves: 384
+    // consecutive rows of the flattened (batch, head, row) range, i.e. of one head or two (two sets, the second copied
+    // only when present); a wave's 32 rows lie in one head (the rows per head are a multiple of 32), and waves past
+    // the last row recompute the last 32 rows without storing them.
+    int b, h, q0, set = 0, kvb[2], kvh[2];
+    bool store = true, two = false;
+    if constexpr (NWV == 4) {
+        const int bh = blk / p.qblocks, qblk = blk % p.qblocks;
+        b = bh / p.H;
+        h = bh % p.H;
+        q0 = qblk * QB + wq * 32;
+        kvb[0] = kvb[1] = b;
+        kvh[0] = kvh[1] = h / (p.H / p.Hkv);
+    } else {
+        const long g0 = (long)blk * FLAT_ROWS, gw = g0 + 32 * wq, gc = gw < p.rows ? gw : p.rows - 32;
+        store = gw < p.rows;
+        const int bh = (int)(gc / p.Lq), bh0 = (int)(g0 / p.Lq), bh1 = (int)((min(g0 + FLAT_ROWS, p.rows) - 1) / p.Lq);
+        b = bh / p.H;
+        h = bh % p.H;
+        q0 = (int)(gc % p.Lq);
+        set = bh - bh0;
+        two = bh1 != bh0;
+        kvb[0] = bh0 / p.H;
+        kvh[0] = (bh0 % p.H) / (p.H / p.Hkv);
+        kvb[1] = bh1 / p.H;
+        kvh[1] = (bh1 % p.H) / (p.H / p.Hkv);
+    }
 
     // Q as the B operand of S^T = K Q^T, for the lane's row q0 + lq.
     h8 qf[8];
@@ -160,51 +191,66 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     for (int i = 0; i < 4; i++) o[i] = (f16v){};
     float m = -1e30f, l = 0.f;
 
-    const half_t* kbase = p.k + b * p.skb + hk * p.skh;
-    const half_t* vbase = p.v + b * p.svb + hk * p.svh;
-    const int bkv = b * p.Hkv + hk;
+    // Copy duty: four waves copy the tile together; of twelve, waves 0-7 copy set 0 and waves 8-11 set 1 (if any).
+    const int cset = NWV == 12 && wq >= 8 ? 1 : 0, cw = wq - 8 * cset;  // the wave's set and index among its copiers
+    const bool copier = cset == 0 || two;
+    const half_t* kbase = p.k + kvb[cset] * p.skb + kvh[cset] * p.skh;
+    const half_t* vbase = p.v + kvb[cset] * p.svb + kvh[cset] * p.svh;
+    const int bkv = kvb[cset] * p.Hkv + kvh[cset];
     const int8_t* k8base = I8 ? p.k8 + (size_t)bkv * p.Lk_pad * 128 : nullptr;
     const float* ksbase = I8 ? p.ks + (size_t)bkv * p.Lk_pad : nullptr;
     const int tiles = (p.Lk + KB - 1) / KB;
 
-    // Copies the tile at key0 into stage st; DMA i (< 2) of a wave fills K (and V) rows 16 i + row0 .. +3,
-    // row0 = 4 wq + lane / 16 (int8 K: one DMA per wave, rows 8 wq + lane / 8). Rows past Lk re-read row
-    // Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite) values drop out. int8 K is
-    // zero-padded to a whole tile by pack_k_i8. Per-lane byte offsets are fixed; only the tile base moves
-    // (the launcher keeps 32 rows of stride inside 2^31 bytes).
-    const int row0 = 4 * wq + (lane >> 4);
+    // Copies the tile at key0 into stage st, each copying wave its part: DMA i (< 2) of a wave fills K (and V)
+    // rows 16 i + row0 .. +3, row0 = 4 cw + lane / 16; the eight copiers of set 0 among twelve waves take one DMA
+    // each, rows row0 .. + 3 (int8 K: one DMA for each of copiers 0-3, rows 8 cw + lane / 8, and copier 0 the
+    // scales). Rows past Lk re-read row Lk - 1: their scores are masked to -1e30, so P is 0 there and the (finite)
+    // values drop out. int8 K is zero-padded to a whole tile by pack_k_i8. Per-lane byte offsets are fixed; only the
+    // tile base moves (the launcher keeps 32 rows of stride inside 2^31 bytes).
+    constexpr bool ONE = NWV == 12;  // one K and one V DMA for the copiers of set 0 (two otherwise)
+    const bool single = ONE && cset == 0;
+    const int row0 = 4 * cw + (lane >> 4);
     const long skl2 = p.skl * 2, svl2 = p.svl * 2;
-    const int kc = (lane & 15) ^ row0, vc = (lane & 15) ^ ((lane >> 4) << 2);
+    const int kc = (lane & 15) ^ (row0 & 15), vc = (lane & 15) ^ ((lane >> 4) << 2);
     const u32 k_off = (u32)(row0 * skl2) + ((u32)kc << 4);
     const u32 v_off = (u32)(row0 * svl2) + ((u32)vc << 4);
-    const u32 k8_off = (u32)((8 * wq + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
+    const u32 k8_off = (u32)((8 * cw + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
     auto issue = [&](int key0, const char* st) {
+        if (!copier) return;
+        st += cset * T::BYTES;
         if (I8) {
-            dma16((const char*)k8base + (size_t)key0 * 128, k8_off, st + wq * 1024);
-            if (wq == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, st + KB * 128);
+            if (cw < 4) dma16((const char*)k8base + (size_t)key0 * 128, k8_off, st + cw * 1024);
+            if (cw == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, st + KB * 128);
         }
         const char* kt = (const char*)kbase + key0 * skl2;
         const char* vt = (const char*)vbase + key0 * svl2;
         if (key0 + KB <= p.Lk) {
-            if (!I8) {
+            if (single) {
+                if (!I8) dma16(kt, k_off, st + cw * 1024);
+                dma16(vt, v_off, st + T::K_BYTES + cw * 1024);
+            } else {
+                if (!I8) {
 #pragma unroll
-                for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + wq) * 1024);
+                    for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + cw) * 1024);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + cw) * 1024);
             }
-#pragma unroll
-            for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + wq) * 1024);
         } else {
             // The tile's base stays in SGPRs; the lane's row (clamped to Lk - 1) enters through its 32-bit offset. The
             // lane id is read again here (a volatile read the compiler cannot hoist), so that this branch, taken once,
             // holds no registers across the tile loop.
             u32 ln;
             asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
-            const int r0 = 4 * wq + (int)(ln >> 4);
-            const u32 kcl = ((ln & 15) ^ (u32)r0) << 4, vcl = ((ln & 15) ^ ((ln >> 4) << 2)) << 4;
+            const int r0 = 4 * cw + (int)(ln >> 4);
+            const u32 kcl = ((ln & 15) ^ (u32)(r0 & 15)) << 4, vcl = ((ln & 15) ^ ((ln >> 4) << 2)) << 4;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                const u32 r = (u32)(min(key0 + 16 * i + r0, p.Lk - 1) - key0);
-                if (!I8) dma16(kt, r * (u32)skl2 + kcl, st + (4 * i + wq) * 1024);
-                dma16(vt, r * (u32)svl2 + vcl, st + T::K_BYTES + (4 * i + wq) * 1024);
+                if (single && i > 0) break;
+                const int ri = single ? r0 : 16 * i + r0, di = single ? cw : 4 * i + cw;
+                const u32 r = (u32)(min(key0 + ri, p.Lk - 1) - key0);
+                if (!I8) dma16(kt, r * (u32)skl2 + kcl, st + di * 1024);
+                dma16(vt, r * (u32)svl2 + vcl, st + T::K_BYTES + di * 1024);
             }
         }
     };
@@ -216,8 +262,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     u32 ks_rd = 0;
     if (I8) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) k_rd[ks] = (u32)(lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
-        ks_rd = (u32)(KB * 128 + 16 * g);
+        for (int ks = 0; ks < 4; ks++) k_rd[ks] = (u32)(set * T::BYTES + lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+        ks_rd = (u32)(set * T::BYTES + KB * 128 + 16 * g);
         asm volatile("" : "+v"(ks_rd));
     }
     const u32 smem_u = lds_addr(smem);  // the dynamic LDS base (0: no static LDS), folded into the per-lane offsets below
@@ -226,7 +272,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     u32 v_base;
     {
         const int sg = lane & 15;
-        const u32 vt = smem_u + (u32)(T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
+        const u32 vt = smem_u + (u32)(set * T::BYTES + T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
         const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);
         v_base = vt + (u32)(vx << 4);
     }
@@ -238,7 +284,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // The fp16 K reads of a lane: row lq of the stage, chunk 2 ks + g at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx, i.e. byte
     // offset 256 lq + ((kx << 4) ^ 32 ks). The dynamic LDS starts at offset 0 (this kernel has no static LDS), so the
     // low eight bits of k_base are kx << 4 and the read for ks is k_base ^ 32 ks: one xor per read from one value.
-    u32 k_base = smem_u + (u32)(lq * 256) + (u32)(((lane & 15) ^ g) << 4);
+    u32 k_base = smem_u + (u32)(set * T::BYTES + lq * 256) + (u32)(((lane & 15) ^ g) << 4);
     asm volatile("" : "+v"(k_base));
 
     // S^T of the tile in stage `stage` (a compile-time stage folds into the reads' offset fields; a runtime one is
@@ -246,7 +292,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // four int8 ones): the caller puts the previous tile's exponentials there, which the transcendental unit runs
     // while the matrix cores work on these products.
     auto qk = [&](auto stage, float (&out)[16], auto&& hook) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * T::BYTES);
+        const u32 st_u = (u32)((int)stage * SS);
         if constexpr (!I8) {
             // K operands of the first 64 dims go out before the products; each operand of the second 64 is read into
             // the registers the matching first-half product has just consumed. The base passes through an empty asm
@@ -356,7 +402,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     // O^T += V^T P^T with the V tile of stage `stage` and P in pf. Each V^T operand of the second 16-key step is read
     // into the registers the matching first-step product has just consumed.
     auto pv = [&](auto stage) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * T::BYTES);
+        const u32 st_u = (u32)((int)stage * SS);
         u32 vb = v_base;
         asm volatile("" : "+v"(vb));
         auto read_v = [&](int j, int dt) __attribute__((always_inline)) {
@@ -395,7 +441,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
     auto step = [&](int i, auto stage, auto kind) __attribute__((always_inline)) {
         constexpr int K = decltype(kind)::value;
         const auto next = next_stage(stage);
-        if constexpr (K == 0) issue((i + 2) * KB, smem + (int)next_stage(next) * T::BYTES);
+        if constexpr (K == 0) issue((i + 2) * KB, smem + (int)next_stage(next) * SS);
         const float l_old = l;
         if constexpr (K != 2) {
             float nxt[16];
@@ -417,8 +463,8 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
         }
     };
     const int first = ((1 - tiles) % 3 + 3) % 3;  // the stage of tile 0
-    issue(0, smem + first * T::BYTES);
-    if (tiles > 1) issue(KB, smem + next_stage(first) * T::BYTES);
+    issue(0, smem + first * SS);
+    if (tiles > 1) issue(KB, smem + next_stage(first) * SS);
     wait_copies();
     __syncthreads();
     if (tiles == 1) {
@@ -457,7 +503,7 @@ __global__ __launch_bounds__(AT) __attribute__((amdgpu_waves_per_eu(3, 3))) void
             h4v w;
 #pragma unroll
             for (int e = 0; e < 4; e++) w[e] = to_half(o[dt][r4 * 4 + e] * inv);
-            if (row < p.Lq) *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
+            if (store && row < p.Lq) *(h4v*)(op + dt * 32 + 8 * r4 + 4 * g) = w;
         }
 }
 
@@ -511,6 +557,7 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, void* out
     a.Lk_pad = (Lk + KB - 1) / KB * KB;
     a.qblocks = (Lq + QB - 1) / QB;
     a.nblocks = a.qblocks * B * H;
+    a.rows = (long)B * H * Lq;
     a.sqb = st[0]; a.sqh = st[1]; a.sql = st[2];
     a.skb = st[3]; a.skh = st[4]; a.skl = st[5];
     a.svb = st[6]; a.svh = st[7]; a.svl = st[8];
@@ -519,13 +566,24 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, void* out
     return a;
 }
 
-template <bool I8>
-static int launch_attn(const AttnArgs& a, void* stream) {
-    const size_t lds = Tile<I8>::LDS;
+template <bool I8, int NWV>
+static int launch_attn_waves(const AttnArgs& a, void* stream) {
+    constexpr size_t lds = attn_lds<I8, NWV>();
     static std::atomic<size_t> configured[RDA_MAX_DEVICES];
-    if (const int e = ensure_dynamic_lds((const void*)attn_kernel<I8>, lds, configured)) return e;
-    hipLaunchKernelGGL(attn_kernel<I8>, dim3(a.nblocks), dim3(AT), lds, (hipStream_t)stream, a);
+    if (const int e = ensure_dynamic_lds((const void*)attn_kernel<I8, NWV>, lds, configured)) return e;
+    hipLaunchKernelGGL((attn_kernel<I8, NWV>), dim3(a.nblocks), dim3(64 * NWV), lds, (hipStream_t)stream, a);
     return (int)hipGetLastError();
+}
+
+// Twelve-wave workgroups when every head's rows are a multiple of 32 (a wave's rows then lie in one head) and at
+// least 384 (a workgroup's rows then span at most two heads); four-wave ones otherwise.
+template <bool I8>
+static int launch_attn(AttnArgs a, void* stream) {
+    if (a.Lq % 32 == 0 && a.Lq >= FLAT_ROWS) {
+        a.nblocks = (int)((a.rows + FLAT_ROWS - 1) / FLAT_ROWS);
+        return launch_attn_waves<I8, 12>(a, stream);
+    }
+    return launch_attn_waves<I8, 4>(a, stream);
 }
 
 // Row strides of K and V must keep a tile's 32 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
