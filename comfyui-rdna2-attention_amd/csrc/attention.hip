@@ -13,9 +13,9 @@
 // settle below): the outcome is the same as computing it for every tile.
 //
 // Work split. Each wave owns 32 query rows and walks the whole key range, keeping Q, O, l and m for
-// its rows in registers (<= 168 VGPRs, three waves per SIMD). When every head has a multiple of 32
-// query rows and at least 384, a workgroup is twelve waves over 384 consecutive rows of the rows
-// flattened over (batch, head, row), one workgroup per CU: the attention configuration (24 heads x
+// its rows in registers (<= 168 VGPRs, three waves per SIMD). When every head has at least 384 query
+// rows, a workgroup is twelve waves over 384 consecutive rows of the rows flattened over (batch,
+// head, row), each head's padded to a multiple of 32, one workgroup per CU: the attention configuration (24 heads x
 // 4096 rows) is 256 workgroups, one round, and each K/V tile is copied once for twelve waves rather
 // than once per four (copies measured at ~8% of the kernel). A workgroup's rows then lie in one head
 // or two; with two it keeps a second set of tiles, copied by waves 8-11 (waves 0-7 copy the first),
@@ -58,7 +58,8 @@ struct AttnArgs {
     const int8_t* k8;  // int8 K [B * Hkv][Lk_pad][128]
     const float* ks;   // per-key scales [B * Hkv][Lk_pad]
     int H, Hkv, Lq, Lk, Lk_pad, qblocks, nblocks;
-    long rows;  // B H Lq, the query rows flattened over (batch, head, row)
+    int Lq_pad;  // Lq rounded up to 32: the rows of a head in the flattened range
+    long rows;   // B H Lq_pad, the query rows flattened over (batch, head, row)
     long sqb, sqh, sql, skb, skh, skl, svb, svh, svl, sob, soh, sol;
     float scale_log2;
 };
@@ -110,9 +111,9 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     if (p.nblocks % 8 == 0) blk = (blk % 8) * (p.nblocks / 8) + blk / 8;
     // The wave's query rows q0 .. q0 + 31 of head h of batch b. Tile set c of the workgroup holds the K/V of batch
     // kvb[c], KV head kvh[c]; the wave reads set `set`. Four waves: one set, 128 rows of one head. Twelve waves: 384
-    // consecutive rows of the flattened (batch, head, row) range, i.e. of one head or two (two sets, the second copied
-    // only when present); a wave's 32 rows lie in one head (the rows per head are a multiple of 32), and waves past
-    // the last row recompute the last 32 rows without storing them.
+    // consecutive rows of the (batch, head, row) range with each head's rows padded to a multiple of 32 (Lq_pad), i.e.
+    // of one head or two (two sets, the second copied only when present); a wave's 32 rows lie in one head, padding
+    // rows recompute row Lq - 1 and waves past the last row the last 32 rows, neither stored.
     int b, h, q0, set = 0, kvb[2], kvh[2];
     bool store = true, two = false;
     if constexpr (NWV == 4) {
@@ -125,10 +126,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     } else {
         const long g0 = (long)blk * FLAT_ROWS, gw = g0 + 32 * wq, gc = gw < p.rows ? gw : p.rows - 32;
         store = gw < p.rows;
-        const int bh = (int)(gc / p.Lq), bh0 = (int)(g0 / p.Lq), bh1 = (int)((min(g0 + FLAT_ROWS, p.rows) - 1) / p.Lq);
+        const int bh = (int)(gc / p.Lq_pad), bh0 = (int)(g0 / p.Lq_pad), bh1 = (int)((min(g0 + FLAT_ROWS, p.rows) - 1) / p.Lq_pad);
         b = bh / p.H;
         h = bh % p.H;
-        q0 = (int)(gc % p.Lq);
+        q0 = (int)(gc % p.Lq_pad);
         set = bh - bh0;
         two = bh1 != bh0;
         kvb[0] = bh0 / p.H;
@@ -557,7 +558,8 @@ static AttnArgs make_args(const void* q, const void* k, const void* v, void* out
     a.Lk_pad = (Lk + KB - 1) / KB * KB;
     a.qblocks = (Lq + QB - 1) / QB;
     a.nblocks = a.qblocks * B * H;
-    a.rows = (long)B * H * Lq;
+    a.Lq_pad = (Lq + 31) / 32 * 32;
+    a.rows = (long)B * H * a.Lq_pad;
     a.sqb = st[0]; a.sqh = st[1]; a.sql = st[2];
     a.skb = st[3]; a.skh = st[4]; a.skl = st[5];
     a.svb = st[6]; a.svh = st[7]; a.svl = st[8];
@@ -575,11 +577,11 @@ static int launch_attn_waves(const AttnArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-// Twelve-wave workgroups when every head's rows are a multiple of 32 (a wave's rows then lie in one head) and at
-// least 384 (a workgroup's rows then span at most two heads); four-wave ones otherwise.
+// Twelve-wave workgroups when every head has at least 384 query rows (a workgroup's rows, each head's padded to a
+// multiple of 32, then span at most two heads); four-wave ones otherwise.
 template <bool I8>
 static int launch_attn(AttnArgs a, void* stream) {
-    if (a.Lq % 32 == 0 && a.Lq >= FLAT_ROWS) {
+    if (a.Lq >= FLAT_ROWS) {
         a.nblocks = (int)((a.rows + FLAT_ROWS - 1) / FLAT_ROWS);
         return launch_attn_waves<I8, 12>(a, stream);
     }
