@@ -354,7 +354,10 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
     // clamped in bounds so that no load sits under a branch; the first batch goes out before the dequantization
     // pass, whose LDS work then covers its latency. (One load per chunk, each awaited before its store, left
     // the epilogue latency-bound: +17 us on 4096 x 3072 x 3072.)
-    constexpr int RB = ITER % 8 == 0 ? 8 : ITER % 4 == 0 ? 4 : 1, NBATCH = ITER / RB;
+    // A batch is 16 VGPRs per chunk, and the first is in flight while the accumulators are live: eight-wave tiles of
+    // 64 x 128 (128 accumulator VGPRs of a 256 budget) take batches of 4.
+    constexpr int RBMAX = NT >= 512 && FI * FJ >= 8 ? 4 : 8;
+    constexpr int RB = ITER % RBMAX == 0 ? RBMAX : ITER % 4 == 0 ? 4 : 1, NBATCH = ITER / RB;
     h8 res[2][RB], gat[2][RB];
     auto load = [&](int b, int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -836,7 +839,10 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
         const bool wide = K % 128 == 0;
         if (W4 && !wide) return -1;
         switch (gemm8_width(M, N) * 2 + (wide ? 1 : 0)) {
-            case 513: return launch_gemm8<256, 256, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            // int8 weights: eight waves of 64 x 128 (4096 x 8192 x 3072: 91.1-92.3 -> 88.4-90.0 us on one box).
+            case 513:
+                if constexpr (!W4) return launch_gemm8<256, 256, 128, 2, false, EPI, 1, 4, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+                else return launch_gemm8<256, 256, 128, 2, W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
             // int8 weights: eight waves of 64 x 96 (two per SIMD, so one wave's fragment and copy waits are covered by the
             // other's products: 39.7 -> 38.6 us at 4096 x 3072 x 3072); int4 weights keep four waves of 128 x 96.
             case 385: return launch_gemm8<256, 192, 128, 2, W4, EPI, 1, (W4 ? 2 : 4), (W4 ? 4 : 8)>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
