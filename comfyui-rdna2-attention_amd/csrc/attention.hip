@@ -292,6 +292,29 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     // added), scaled for int8, into out. hook(k) runs right after the k-th product is issued (eight fp16 products,
     // four int8 ones): the caller puts the previous tile's exponentials there, which the transcendental unit runs
     // while the matrix cores work on these products.
+    // int8: the products of S^T (int32), and a quarter of their scaling -- scores times the per-key scales only; the
+    // per-row factor (Q's scale times scale log2 e) enters the exponent's FMA (exps) and the slow path's maximum. The
+    // steady steps run the scaling of the next tile's scores beside the PV products, where the vector ALU is idle.
+    auto qk_raw = [&](auto stage, i16v& acc, auto&& hook) __attribute__((always_inline)) {
+        const u32 st_u = (u32)((int)stage * SS);
+        i4v ka[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(smem + st_u + k_rd[ks]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc = (i16v){};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
+            hook(ks);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto scale_part = [&](auto stage, const i16v& acc, float (&out)[16], int r4) __attribute__((always_inline)) {
+        const u32 st_u = (u32)((int)stage * SS);
+        const f4 sc = *(const f4*)(smem + st_u + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
+#pragma unroll
+        for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * sc[e];  // hip_attention.hip:227
+    };
     auto qk = [&](auto stage, float (&out)[16], auto&& hook) __attribute__((always_inline)) {
         const u32 st_u = (u32)((int)stage * SS);
         if constexpr (!I8) {
@@ -322,25 +345,10 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
 #pragma unroll
             for (int r = 0; r < 16; r++) out[r] = acc[r];
         } else {
-            i4v ka[4];
+            i16v acc;
+            qk_raw(stage, acc, hook);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(smem + st_u + k_rd[ks]);
-            __builtin_amdgcn_sched_barrier(0);
-            i16v acc = {};
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[ks], q8f[ks], acc, 0, 0, 0);
-                hook(ks);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // Scores times the per-key scales only; the per-row factor (Q's scale times scale log2 e) enters the exponent's
-            // FMA (exps) and the slow path's maximum.
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const f4 sc = *(const f4*)(smem + st_u + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
-#pragma unroll
-                for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * sc[e];  // hip_attention.hip:227
-            }
+            for (int r4 = 0; r4 < 4; r4++) scale_part(stage, acc, out, r4);
         }
     };
     auto no_hook = [](int) {};
@@ -402,7 +410,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     };
     // O^T += V^T P^T with the V tile of stage `stage` and P in pf. Each V^T operand of the second 16-key step is read
     // into the registers the matching first-step product has just consumed.
-    auto pv = [&](auto stage) __attribute__((always_inline)) {
+    auto pv = [&](auto stage, auto&& hook) __attribute__((always_inline)) {
         const u32 st_u = (u32)((int)stage * SS);
         u32 vb = v_base;
         asm volatile("" : "+v"(vb));
@@ -418,6 +426,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
         for (int dt = 0; dt < 4; dt++) {
             o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], pf[0], o[dt], 0, 0, 0);
             va[dt] = read_v(1, dt);
+            hook(dt);
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -446,17 +455,25 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
         const float l_old = l;
         if constexpr (K != 2) {
             float nxt[16];
-            qk(next, nxt, exps);
-            if constexpr (K == 1) mask(nxt, (i + 1) * KB);
-            settle(stage, i * KB, std::false_type{}, l_old);
-            pv(stage);
+            if constexpr (I8) {
+                i16v raw;
+                qk_raw(next, raw, exps);
+                settle(stage, i * KB, std::false_type{}, l_old);
+                pv(stage, [&](int dt) { scale_part(next, raw, nxt, dt); });
+                if constexpr (K == 1) mask(nxt, (i + 1) * KB);
+            } else {
+                qk(next, nxt, exps);
+                if constexpr (K == 1) mask(nxt, (i + 1) * KB);
+                settle(stage, i * KB, std::false_type{}, l_old);
+                pv(stage, no_hook);
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) s[r] = nxt[r];
         } else {
 #pragma unroll
             for (int k = 0; k < PARTS; k++) exps(k);
             settle(stage, i * KB, std::true_type{}, l_old);
-            pv(stage);
+            pv(stage, no_hook);
         }
         if constexpr (K == 0) {
             wait_copies();
