@@ -37,10 +37,11 @@ def gemv_bound(w, x, scale, half):
 
 
 @pytest.mark.parametrize("x_half", [False, True])
-# one row per wave: (4096, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536), (1000, 1536); K split over 4 waves per
-# row: (1024, 4096), (1002, 16384), (8, 4096); over 2: (2048, 8192), (1500, 2048)
+# one row per wave: (4096, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536), (1000, 1536), and with fp16 x read straight
+# into registers (2049-4096 rows, K a multiple of 1024 up to 4096): (4096, 4096), (3000, 2048), (2500, 1024); K split over 4
+# waves per row: (1024, 4096), (1002, 16384), (8, 4096); over 2: (2048, 8192), (1500, 2048)
 @pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (12288, 4096), (64, 512), (4100, 9728), (16, 1536), (1000, 1536), (1002, 16384),
-                                 (8, 1024), (2048, 8192), (1500, 2048)])
+                                 (8, 1024), (2048, 8192), (1500, 2048), (3000, 2048), (2500, 1024)])
 def test_gemv_i8(dev, N, K, x_half):
     print(f"gemv_i8 N={N} K={K} half={x_half}", flush=True)
     x = torch.randn(1, K, generator=gen(16))
