@@ -825,11 +825,9 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
         // The block's group scales are staged whole (BN x K / 128 halves), so past K = 3456 two blocks no longer fit a
         // CU's LDS: then one block per CU, which holds the scales of K up to ~45000.
         if (group != 128 || K % 128 != 0 || N % 128 != 0 || !aligned(gs, 16)) return -1;
-        if (N % 256 == 0) {
-            const int e = launch_gemm8<128, 256, 128, 4, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        if (N % 256 == 0) {  // three stages (four, where they fit, measured 1.4% slower at K = 3072)
+            const int e = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
             if (e >= 0) return e;
-            const int e3 = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
-            if (e3 >= 0) return e3;
         }
         const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
         if (e >= 0) return e;
