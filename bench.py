@@ -663,7 +663,7 @@ F16_BASELINES = ("attention_f16", "attention_i8qk", "w8a8_gemm", "w8a8_linear", 
 
 def cpu_baseline(torch, name, seconds=1.5, **kw):
     """The CPU baseline of workload `name`: cpu_rate() in fp32 and, where the fallback also runs in fp16, in fp16; the
-    faster is `value` (SURVEY-style: label both, headline the faster)."""
+    faster is `value` (both are reported)."""
     rec = cpu_rate(torch, name, seconds, **kw)
     rec["dtype"] = "fp32"
     if name in F16_BASELINES:
