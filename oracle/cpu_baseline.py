@@ -1,6 +1,6 @@
 """The reference's own torch fallbacks, restated for the host CPU -- TEST AND BENCH INFRASTRUCTURE ONLY.
 
-bench.py's cpu_baseline leg times these on the GPU box's host cores beside each GPU workload; tests/test_cpu_baseline.py
+bench.py's cpu_baseline leg times these on the host cores of the machine that runs each GPU workload; tests/test_cpu_baseline.py
 pins each against float64 closed forms. The product (the package comfyui-rdna2-attention_amd) never imports them.
 
 What the reference runs when its kernels do not take a call:
