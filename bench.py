@@ -297,8 +297,9 @@ def w_decode_attention(torch, dev):
 def w_decode_layer(torch, dev):
     """One token through one Qwen3-8B-shaped layer as int8_gemv's patched forwards run it (int8_gemv.py:48-64,
     111-113): hidden 4096, 32 query / 8 KV heads of 128, MLP 12288, KV cache length 2048 (fp32). Each of the seven
-    int8 linears is int8_gemv.linear_forward's single-token path -- the ConvRot of its fp32 input (group 256; q, k
-    and v read one input, as do gate and up, so one rotation serves each group of them) then the GEMV -- with a
+    int8 linears is int8_gemv.linear_forward's single-token path -- the ConvRot of its fp32 input (group 256) and the
+    GEMV: the first linear of an input rotates it inside its GEMV launch and keeps the rotation, which k and v (after
+    q) and up (after gate) reuse; the down projection (K = 12288) rotates then runs the GEMV -- with a
     stand-in for ComfyUI's quantized-weight context handing it the layer's int8 weight; attention is
     int8_gemv.attention_decode; the layer's own torch ops (norms, rope, silu * up, residual adds) are outside this
     path and not included. Replayed from a HIP graph, as a decode loop would, over enough weight and cache copies
@@ -334,8 +335,8 @@ def w_decode_layer(torch, dev):
             s = (torch.rand(n, generator=g) * 2e-3 + 1e-3).float().to(dev)
             pairs[id(mods[name])] = (types.SimpleNamespace(_qdata=w, _params=types.SimpleNamespace(scale=s)), None)
         kv = [torch.randn(1, cap, Hkv, 128, generator=g).float().to(dev) for _ in range(2)]
-        layers.append((mods, kv))
-    x = torch.randn(1, 1, D, generator=g).float().to(dev)
+        # each step's input is a tensor of its own, as each token's is: no rotation carries over between steps
+        layers.append((mods, kv, torch.randn(1, 1, D, generator=g).float().to(dev)))
     lengths = torch.full((1,), cap, dtype=torch.int32, device=dev)
 
     def lin(mods, name, inp):
@@ -343,7 +344,7 @@ def w_decode_layer(torch, dev):
         return int8_gemv.linear_forward(mods[name], n, k, torch.int8, 256, inp)
 
     def step(i):
-        mods, (kc, vc) = layers[i]
+        mods, (kc, vc), x = layers[i]
         q = lin(mods, "q", x)
         lin(mods, "k", x)
         lin(mods, "v", x)

@@ -34,6 +34,147 @@ __global__ __launch_bounds__(256) void rotate_kernel(const float* __restrict__ x
 
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 
+// Position in the GEMVs' LDS copy of x of its f4 number i (values 4i .. 4i + 3), in reading order: the f4 j of lane
+// l in step s at (4s + j) * 64 + l, in the half step past the `steps` whole ones at 256 steps + 64 j + l.
+__device__ __forceinline__ int gemv_pos(int i, int steps) {
+    const int tail = i - steps * 256;
+    return tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1);
+}
+
+// One H4 step of rotate_kernel on the four values i, i + s, i + 2s, i + 3s (elementwise for f4): the same sum order,
+// so the same roundings.
+template <typename T>
+__device__ __forceinline__ void h4_step(T& a, T& b, T& c, T& d) {
+    const T sum = a + b + c + d;
+    const T na = sum - 2.0f * d, nb = sum - 2.0f * c, nc = sum - 2.0f * b, nd = sum - 2.0f * a;
+    a = na;
+    b = nb;
+    c = nc;
+    d = nd;
+}
+
+// The H4 step of stride 1 on the four consecutive values of one f4.
+__device__ __forceinline__ f4 h4_step1(f4 x) {
+    const float sum = x[0] + x[1] + x[2] + x[3];
+    return (f4){sum - 2.0f * x[3], sum - 2.0f * x[2], sum - 2.0f * x[1], sum - 2.0f * x[0]};
+}
+
+// The fused ConvRot of the GEMVs' fp32 x (rotate_kernel's arithmetic, bit for bit) goes through two LDS layouts of
+// one buffer (word = 4 bytes):
+// * natural: value v at word nat_word(v) = v + 4 (v >> 4) + 16 (v >> 8) -- a thread's four f4s of 16 consecutive values
+//   and the transposed words 256 b + 16 i + p (p = lane & 15, b = 4 consecutive blocks a wave) both fall in distinct
+//   banks;
+// * reading order: the f4 j of lane l in step s at ro_f4(s, j, l) = (4 s + j) RO_ROW + l + 4 (l >> 4), the half step
+//   past the `steps` whole ones as step `steps` with j < 2 and 8 values per lane. RO_ROW is odd, so that a transposed
+//   thread set's word writes land in 64 distinct banks, and a product read's 16-lane groups take consecutive f4s.
+#define RO_ROW 77
+__device__ __forceinline__ int ro_f4(int s, int j, int l) { return (4 * s + j) * RO_ROW + l + 4 * (l >> 4); }
+__device__ __forceinline__ int ro_of_value(int v, int steps) {  // the f4 holding value v (a multiple of 4)
+    if (v < steps * 1024) return ro_f4(v >> 10, (v >> 2) & 3, (v >> 4) & 63);
+    const int t = v - steps * 1024;
+    return ro_f4(steps, (t >> 2) & 1, t >> 3);
+}
+// Bytes of LDS the fused rotation needs for K values: the larger of the two layouts.
+static inline size_t rot_lds_bytes(int K) {
+    const int rows = 4 * (K / 1024) + (K % 1024 ? 2 : 0);
+    const size_t nat = (size_t)K + K / 4 + K / 16, ro = (size_t)4 * rows * RO_ROW;
+    return 4 * (nat > ro ? nat : ro);
+}
+
+// The NT threads of the workgroup take x in sets of 16 consecutive values, set q = thread + NT r (r < RS). rot_load
+// issues the loads (before the weights'). rot_to_lds runs the H4 steps of strides 1 and 4 on a set's registers, writes
+// the sets in natural order, and reads them back transposed -- thread u = q takes the 16 values 256 b + 16 i + p of
+// b = u >> 4, p = u & 15 -- for the steps of strides 16 and 64 in registers, and writes the results times
+// 1 / sqrt(group) in reading order once every thread has read: three LDS passes, three barriers with the caller's
+// (groups of 4 and 16 write their sets in reading order straight away). With rot_out (nonzero in one workgroup) the
+// rotated values are also stored there, in natural order. group is 4, 16, 64 or 256: larger groups
+// would need LDS steps of their own (rotate_kernel then gemv_i8_kernel serve them). The caller waits at a barrier
+// before reading xs.
+template <int NT, int RS>
+__device__ __forceinline__ void rot_load(const float* __restrict__ x, int K, f4 (&v)[RS][4]) {
+#pragma unroll
+    for (int r = 0; r < RS; r++) {
+        const int q = threadIdx.x + NT * r;
+        const f4* src = (const f4*)x + 4 * (q < K / 16 ? q : 0);  // sets past K / 16 re-read set 0 and are skipped
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[r][j] = src[j];
+    }
+}
+
+template <int NT, int RS>
+__device__ __forceinline__ void rot_to_lds(f4 (&v)[RS][4], f4* xs, int K, int group, int steps, float* __restrict__ rot_out) {
+    float* xw = (float*)xs;
+    const int sets = K / 16;
+    const float norm = 1.0f / sqrtf((float)group);
+#pragma unroll
+    for (int r = 0; r < RS; r++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[r][j] = h4_step1(v[r][j]);  // stride 1
+        if (group >= 16) h4_step(v[r][0], v[r][1], v[r][2], v[r][3]);  // stride 4
+    }
+    if (group <= 16) {
+#pragma unroll
+        for (int r = 0; r < RS; r++) {
+            const int q = threadIdx.x + NT * r;
+            if (q < sets)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const f4 val = v[r][j] * norm;
+                    xs[ro_of_value(16 * q + 4 * j, steps)] = val;
+                    if (rot_out) ((f4*)rot_out)[4 * q + j] = val;
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < RS; r++) {
+        const int q = threadIdx.x + NT * r;
+        if (q < sets)
+#pragma unroll
+            for (int j = 0; j < 4; j++) *(f4*)(xw + 20 * q + 16 * (q >> 4) + 4 * j) = v[r][j];  // nat_word(16 q + 4 j)
+    }
+    __syncthreads();
+    float y[RS][16];
+#pragma unroll
+    for (int r = 0; r < RS; r++) {
+        const int u = threadIdx.x + NT * r;
+        if (u < sets) {
+            const float* src = xw + 336 * (u >> 4) + (u & 15);  // nat_word(256 b + p + 16 i) = 336 b + p + 20 i
+#pragma unroll
+            for (int i = 0; i < 16; i++) y[r][i] = src[20 * i];
+#pragma unroll
+            for (int k = 0; k < 4; k++) h4_step(y[r][4 * k], y[r][4 * k + 1], y[r][4 * k + 2], y[r][4 * k + 3]);  // stride 16
+            if (group >= 256)
+#pragma unroll
+                for (int m = 0; m < 4; m++) h4_step(y[r][m], y[r][m + 4], y[r][m + 8], y[r][m + 12]);  // stride 64
+        }
+    }
+    __syncthreads();  // every transposed read done: the reading order overwrites the buffer
+    {
+#pragma unroll
+        for (int r = 0; r < RS; r++) {
+            const int u = threadIdx.x + NT * r, b = u >> 4, p = u & 15;
+            if (u < sets) {
+                // value 256 b + 16 i + p: in a whole step s = b / 4, lane 16 (b & 3) + i, f4 p / 4, i.e. word
+                // 4 ((4 s + p / 4) RO_ROW + 20 (b & 3)) + p % 4 + 4 i; in the half step (b >= 4 steps), lane
+                // 32 (b - 4 steps) + 2 i + p / 8, f4 (p / 4) & 1, i.e. word 4 ((4 steps + (p / 4) & 1) RO_ROW
+                // + 40 (b - 4 steps) + p / 8) + p % 4 + 8 i + 16 (i / 8). One formula for both (a wave's four
+                // blocks lie all in whole steps or all in the half step): word0 + di i + dh (i / 8).
+                const bool half = b >= 4 * steps;
+                const int word0 = half ? 4 * ((4 * steps + ((p >> 2) & 1)) * RO_ROW + 40 * (b - 4 * steps) + (p >> 3)) + (p & 3)
+                                       : 4 * ((4 * (b >> 2) + (p >> 2)) * RO_ROW + 20 * (b & 3)) + (p & 3);
+                const int di = half ? 8 : 4, dh = half ? 16 : 0;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float val = y[r][i] * norm;
+                    xw[word0 + di * i + dh * (i >> 3)] = val;
+                    if (rot_out) rot_out[256 * b + 16 * i + p] = val;
+                }
+            }
+        }
+    }
+}
+
 // out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns one row
 // and reads it in steps of 1024 values (16 per lane), plus a last half step of 512 (8 per lane) when
 // TAIL (K % 1024 == 512). x is fp32 or fp16; out has the dtype of x. One row per wave and 8 waves per
@@ -48,10 +189,14 @@ __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w <<
 // chunk of the row and are skipped by the products, indices of x past K / 4 re-read x[0 .. 4).
 // x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the
 // f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
-template <int G, bool TAIL, bool XH>
+// ROT: x (fp32) is first rotated in groups of `group` by the workgroup (rot_to_lds), bit for bit as rotate_kernel
+// would, so that one launch replaces rotate + GEMV; its loads go out before the weights' as well.
+template <int G, bool TAIL, bool XH, bool ROT>
 __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
-                                                                 const float* __restrict__ bias, void* __restrict__ out, int N, int K) {
-    constexpr int XS = (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;  // float4s of x per thread: K / 4 <= 64 GI_WAVES XS
+                                                                 const float* __restrict__ bias, void* __restrict__ out, int N, int K, int group,
+                                                                 float* __restrict__ rot_out) {
+    constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;  // float4s of x per thread: K / 4 <= 64 GI_WAVES XS
+    constexpr int RS = (64 * G + (TAIL ? 32 : 0) + GI_WAVES * 64 - 1) / (GI_WAVES * 64) < 2 ? 1 : 2;  // ROT: sets of 16 per thread, K <= 16384
     extern __shared__ f4 xs[];
     const int steps = K / 1024;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -60,10 +205,15 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
     const int8_t* base = w + (size_t)(active ? row : 0) * K;
     typedef typename std::conditional<XH, h4v, f4>::type xv_t;
     xv_t xr[XS];
+    f4 xq[RS][4];
+    if constexpr (ROT) {
+        rot_load<GI_WAVES * 64, RS>((const float*)xin, K, xq);
+    } else {
 #pragma unroll
-    for (int j = 0; j < XS; j++) {
-        const int i = threadIdx.x + j * GI_WAVES * 64;
-        xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
+        for (int j = 0; j < XS; j++) {
+            const int i = threadIdx.x + j * GI_WAVES * 64;
+            xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
+        }
     }
     const float sc = scale[active ? row : 0];
     __builtin_amdgcn_sched_barrier(0);  // x and the scale go out before the weights
@@ -77,15 +227,18 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
     if constexpr (TAIL) vt = __builtin_nontemporal_load((const u2v*)(base + steps * 1024 + lane * 8));
     __builtin_amdgcn_sched_barrier(0);
 
+    if constexpr (ROT) {
+        rot_to_lds<GI_WAVES * 64, RS>(xq, xs, K, group, steps, blockIdx.x == 0 ? rot_out : nullptr);
+    } else {
 #pragma unroll
-    for (int j = 0; j < XS; j++) {
-        const int i = threadIdx.x + j * GI_WAVES * 64;
-        if (i < K / 4) {
-            const int tail = i - steps * 256;
-            f4 x;
-            if constexpr (XH) x = (f4){(float)xr[j][0], (float)xr[j][1], (float)xr[j][2], (float)xr[j][3]};
-            else x = xr[j];
-            xs[tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1)] = x;
+        for (int j = 0; j < XS; j++) {
+            const int i = threadIdx.x + j * GI_WAVES * 64;
+            if (i < K / 4) {
+                f4 x;
+                if constexpr (XH) x = (f4){(float)xr[j][0], (float)xr[j][1], (float)xr[j][2], (float)xr[j][3]};
+                else x = xr[j];
+                xs[gemv_pos(i, steps)] = x;
+            }
         }
     }
     __syncthreads();
@@ -96,7 +249,7 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
         if (g >= steps) continue;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const f4 xv = xs[(g * 4 + j) * 64 + lane];
+            const f4 xv = xs[ROT ? ro_f4(g, j, lane) : (g * 4 + j) * 64 + lane];
 #pragma unroll
             for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[g][j], i), xv[i], acc);
         }
@@ -104,7 +257,7 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
     if constexpr (TAIL) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const f4 xv = xs[steps * 256 + j * 64 + lane];
+            const f4 xv = xs[ROT ? ro_f4(steps, j, lane) : steps * 256 + j * 64 + lane];
 #pragma unroll
             for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[j], i), xv[i], acc);
         }
@@ -123,12 +276,16 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
 // 16 weights and 16 values of x per step straight into registers (no LDS copy of x: a wave reads only its own K / S
 // slice of it). All loads of the wave are issued first, x then weights, in step order. The S partial sums of a row
 // meet in LDS and are added in part order by the row's first wave. K == 1024 S G.
-template <int S, int G, bool XH>
+// ROT: x (fp32) is rotated in groups of `group` by the whole workgroup into LDS first (rot_to_lds, as in
+// gemv_i8_kernel), and each wave reads its slice from there.
+template <int S, int G, bool XH, bool ROT>
 __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_split_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w,
                                                                        const float* __restrict__ scale, const float* __restrict__ bias,
-                                                                       void* __restrict__ out, int N, int K) {
+                                                                       void* __restrict__ out, int N, int K, int group, float* __restrict__ rot_out) {
     constexpr int RPB = GI_WAVES / S;  // rows per block
+    constexpr int RS = S * G * 64 > GI_WAVES * 64 ? 2 : 1;  // ROT: sets of 16 values per thread (K / 16 = 64 S G <= 1024)
     __shared__ float part_s[GI_WAVES];
+    extern __shared__ f4 xs[];  // ROT: the rotated x in reading order (ro_f4)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * RPB + wave / S, part = wave % S;
     const bool active = row < N;
@@ -136,11 +293,16 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_split_kernel(const void
     const int k0 = part * G * 1024 + lane * 16;  // first of the lane's 16 values of x in step 0
     typedef typename std::conditional<XH, h8, f4>::type xv_t;
     constexpr int XV = XH ? 2 : 4;  // vectors of x per step: 16 values
-    xv_t xr[G][XV];
+    xv_t xr[ROT ? 1 : G][XV];
+    f4 xq[RS][4];
+    if constexpr (ROT) {
+        rot_load<GI_WAVES * 64, RS>((const float*)xin, K, xq);
+    } else {
 #pragma unroll
-    for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int j = 0; j < XV; j++) xr[g][j] = ((const xv_t*)xin)[(k0 + g * 1024) / (16 / XV) + j];
+            for (int j = 0; j < XV; j++) xr[g][j] = ((const xv_t*)xin)[(k0 + g * 1024) / (16 / XV) + j];
+    }
     const float sc = scale[active ? row : 0];
     __builtin_amdgcn_sched_barrier(0);
     u4v v[G];
@@ -149,14 +311,27 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_split_kernel(const void
         v[g] = __builtin_nontemporal_load((const u4v*)(base + g * 1024));
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (ROT) {
+        rot_to_lds<GI_WAVES * 64, RS>(xq, xs, K, group, K / 1024, blockIdx.x == 0 ? rot_out : nullptr);
+        __syncthreads();
+    }
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < G; g++) {
         float xf[16];
+        if constexpr (ROT) {
 #pragma unroll
-        for (int j = 0; j < XV; j++)
+            for (int j = 0; j < 4; j++) {
+                const f4 xv = xs[ro_f4(part * G + g, j, lane)];  // values k0 + 1024 g + 4 j .. + 3
 #pragma unroll
-            for (int e = 0; e < 16 / XV; e++) xf[j * (16 / XV) + e] = (float)xr[g][j][e];
+                for (int e = 0; e < 4; e++) xf[j * 4 + e] = xv[e];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XV; j++)
+#pragma unroll
+                for (int e = 0; e < 16 / XV; e++) xf[j * (16 / XV) + e] = (float)xr[g][j][e];
+        }
 #pragma unroll
         for (int d = 0; d < 4; d++)
 #pragma unroll
@@ -383,30 +558,90 @@ __global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restric
     out[head * HEAD + threadIdx.x] = value / total;
 }
 
-template <int G, bool TAIL, bool XH>
-static int launch_gemv(const void* x, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
-    hipLaunchKernelGGL((gemv_i8_kernel<G, TAIL, XH>), dim3((N + GI_WAVES - 1) / GI_WAVES), dim3(GI_WAVES * 64), (size_t)K * 4, (hipStream_t)stream, x,
-                       (const int8_t*)w, scale, bias, out, N, K);
+template <int G, bool TAIL, bool XH, bool ROT>
+static int launch_gemv(const void* x, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out, void* stream) {
+    const size_t lds = ROT ? rot_lds_bytes(K) : (size_t)K * 4;
+    if constexpr (ROT) {  // K > 12288: more than 64 KiB
+        static std::atomic<size_t> done[RDA_MAX_DEVICES];
+        if (const int e = ensure_dynamic_lds((const void*)gemv_i8_kernel<G, TAIL, XH, ROT>, lds, done)) return e;
+    }
+    hipLaunchKernelGGL((gemv_i8_kernel<G, TAIL, XH, ROT>), dim3((N + GI_WAVES - 1) / GI_WAVES), dim3(GI_WAVES * 64), lds, (hipStream_t)stream, x,
+                       (const int8_t*)w, scale, bias, out, N, K, group, rot_out);
     return (int)hipGetLastError();
 }
 
-template <int S, int G>
-static int launch_gemv_split(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
+template <int S, int G, bool ROT>
+static int launch_gemv_split(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out,
+                             void* stream) {
     constexpr int RPB = GI_WAVES / S;
     const dim3 grid((N + RPB - 1) / RPB), block(GI_WAVES * 64);
-    if (x_half) hipLaunchKernelGGL((gemv_i8_split_kernel<S, G, true>), grid, block, 0, (hipStream_t)stream, x, (const int8_t*)w, scale, bias, out, N, K);
-    else hipLaunchKernelGGL((gemv_i8_split_kernel<S, G, false>), grid, block, 0, (hipStream_t)stream, x, (const int8_t*)w, scale, bias, out, N, K);
+    const size_t lds = ROT ? rot_lds_bytes(K) : 0;
+    if (x_half) {
+        if constexpr (ROT) return RDA_ERR_INVALID;  // the rotation takes fp32 x only
+        else hipLaunchKernelGGL((gemv_i8_split_kernel<S, G, true, false>), grid, block, 0, (hipStream_t)stream, x, (const int8_t*)w, scale, bias, out, N, K, 0, nullptr);
+    } else {
+        if constexpr (ROT) {  // K > 12288: more than 64 KiB
+            static std::atomic<size_t> done[RDA_MAX_DEVICES];
+            if (const int e = ensure_dynamic_lds((const void*)gemv_i8_split_kernel<S, G, false, true>, lds, done)) return e;
+        }
+        hipLaunchKernelGGL((gemv_i8_split_kernel<S, G, false, ROT>), grid, block, lds, (hipStream_t)stream, x, (const int8_t*)w, scale, bias, out, N, K,
+                           group, rot_out);
+    }
     return (int)hipGetLastError();
 }
 
-template <int G>
-static int launch_gemv_g(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
-    switch ((K % 1024 ? 2 : 0) + (x_half ? 1 : 0)) {
-    case 0: return launch_gemv<G, false, false>(x, w, scale, bias, out, N, K, stream);
-    case 1: return launch_gemv<G, false, true>(x, w, scale, bias, out, N, K, stream);
-    case 2: return launch_gemv<G, true, false>(x, w, scale, bias, out, N, K, stream);
-    default: return launch_gemv<G, true, true>(x, w, scale, bias, out, N, K, stream);
+template <int G, bool ROT>
+static int launch_gemv_g(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out,
+                         void* stream) {
+    if constexpr (ROT) {
+        if (K % 1024) return launch_gemv<G, true, false, true>(x, w, scale, bias, out, N, K, group, rot_out, stream);
+        return launch_gemv<G, false, false, true>(x, w, scale, bias, out, N, K, group, rot_out, stream);
+    } else {
+        switch ((K % 1024 ? 2 : 0) + (x_half ? 1 : 0)) {
+        case 0: return launch_gemv<G, false, false, false>(x, w, scale, bias, out, N, K, 0, nullptr, stream);
+        case 1: return launch_gemv<G, false, true, false>(x, w, scale, bias, out, N, K, 0, nullptr, stream);
+        case 2: return launch_gemv<G, true, false, false>(x, w, scale, bias, out, N, K, 0, nullptr, stream);
+        default: return launch_gemv<G, true, true, false>(x, w, scale, bias, out, N, K, 0, nullptr, stream);
+        }
     }
+}
+
+// The GEMV launch of rda_gemv_i8 (ROT false) and rda_rotate_gemv_i8 (ROT true, fp32 x): arguments already checked.
+template <bool ROT>
+static int gemv_i8_dispatch(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out,
+                            void* stream) {
+    const int steps = K / 1024;
+    // Up to 2048 rows, split K: 4 waves per row up to 1024 rows, 2 up to 2048 (K = 4096: N = 1024 3.56 -> 3.01 us;
+    // from 4096 rows on, one row per wave already gives every CU two or more blocks and measured as fast or faster).
+    if (K % 1024 == 0 && N <= 2048) {
+        const int S = N <= 1024 ? 4 : 2;
+        if (steps % S == 0) {
+            switch (S * 100 + steps / S) {
+            case 401: return launch_gemv_split<4, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 402: return launch_gemv_split<4, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 404: return launch_gemv_split<4, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 201: return launch_gemv_split<2, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 202: return launch_gemv_split<2, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 204: return launch_gemv_split<2, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            case 208: return launch_gemv_split<2, 8, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+            default: break;
+            }
+        }
+    }
+    // fp16 x up to 4096 rows: one row per wave with the lane's x read straight into registers (the split kernel with
+    // one part; K = 4096: N = 4096 5.43 -> 5.32 us, bit-identical; at N = 12288 the LDS copy of x is faster).
+    if (!ROT && x_half && N <= 4096 && K % 1024 == 0) {
+        switch (steps) {
+        case 1: return launch_gemv_split<1, 1, false>(x, x_half, w, scale, bias, out, N, K, 0, nullptr, stream);
+        case 2: return launch_gemv_split<1, 2, false>(x, x_half, w, scale, bias, out, N, K, 0, nullptr, stream);
+        case 4: return launch_gemv_split<1, 4, false>(x, x_half, w, scale, bias, out, N, K, 0, nullptr, stream);
+        default: break;
+        }
+    }
+    // One row per wave. Steps in flight: the first of 4, 8, 16 that covers K / 1024.
+    if (steps <= 4) return launch_gemv_g<4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+    if (steps <= 8) return launch_gemv_g<8, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+    return launch_gemv_g<16, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
 }
 
 extern "C" {
@@ -420,38 +655,17 @@ int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
 // x_half: 0 for fp32 x and out, 1 for fp16 x and out.
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
     if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
-    const int steps = K / 1024;
-    // Up to 2048 rows, split K: 4 waves per row up to 1024 rows, 2 up to 2048 (K = 4096: N = 1024 3.56 -> 3.01 us;
-    // from 4096 rows on, one row per wave already gives every CU two or more blocks and measured as fast or faster).
-    if (K % 1024 == 0 && N <= 2048) {
-        const int S = N <= 1024 ? 4 : 2;
-        if (steps % S == 0) {
-            switch (S * 100 + steps / S) {
-            case 401: return launch_gemv_split<4, 1>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 402: return launch_gemv_split<4, 2>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 404: return launch_gemv_split<4, 4>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 201: return launch_gemv_split<2, 1>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 202: return launch_gemv_split<2, 2>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 204: return launch_gemv_split<2, 4>(x, x_half, w, scale, bias, out, N, K, stream);
-            case 208: return launch_gemv_split<2, 8>(x, x_half, w, scale, bias, out, N, K, stream);
-            default: break;
-            }
-        }
-    }
-    // fp16 x up to 4096 rows: one row per wave with the lane's x read straight into registers (the split kernel with
-    // one part; K = 4096: N = 4096 5.43 -> 5.32 us, bit-identical; at N = 12288 the LDS copy of x is faster).
-    if (x_half && N <= 4096 && K % 1024 == 0) {
-        switch (steps) {
-        case 1: return launch_gemv_split<1, 1>(x, x_half, w, scale, bias, out, N, K, stream);
-        case 2: return launch_gemv_split<1, 2>(x, x_half, w, scale, bias, out, N, K, stream);
-        case 4: return launch_gemv_split<1, 4>(x, x_half, w, scale, bias, out, N, K, stream);
-        default: break;
-        }
-    }
-    // One row per wave. Steps in flight: the first of 4, 8, 16 that covers K / 1024.
-    if (steps <= 4) return launch_gemv_g<4>(x, x_half, w, scale, bias, out, N, K, stream);
-    if (steps <= 8) return launch_gemv_g<8>(x, x_half, w, scale, bias, out, N, K, stream);
-    return launch_gemv_g<16>(x, x_half, w, scale, bias, out, N, K, stream);
+    return gemv_i8_dispatch<false>(x, x_half, w, scale, bias, out, N, K, 0, nullptr, stream);
+}
+
+// rotate then gemv_i8 in one launch (fp32 x and out): the same outputs, bit for bit, as rda_rotate of x's K / group
+// groups followed by rda_gemv_i8 of the result; `rotated` (K floats, or null) receives that rotation as well, written
+// by the first workgroup.
+int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* scale, const float* bias, float* out, float* rotated, int N, int K,
+                       void* stream) {
+    if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
+    if (group != 4 && group != 16 && group != 64 && group != 256) return RDA_ERR_INVALID;
+    return gemv_i8_dispatch<true>(x, 0, w, scale, bias, out, N, K, group, rotated, stream);
 }
 
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream) {

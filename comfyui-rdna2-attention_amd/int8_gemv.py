@@ -30,6 +30,10 @@ SPLITS = 32  # position chunks per KV head in attn_decode (SPLITS in csrc/decode
 GROUPS = 4  # query heads per KV head that patch() requires
 HEAD = 128
 FAST_DEQUANT_GROUP = 256  # Larger ConvRot groups make kitchen's dequantize fall back to a dense matmul.
+FUSED_ROTATION_GROUPS = (4, 16, 64, 256)  # ConvRot groups that rotate_gemv rotates inside the GEMV's launch
+# linear_forward fuses the rotation up to this K: past it the GEMV holds 16 weight steps per lane and the rotation's
+# registers leave one workgroup per CU (K = 12288: 16.3 us fused against 14.6 us for rotate then GEMV)
+FUSED_ROTATION_MAX_K = 8192
 
 kernels = None
 # True inside generate(): prompt encoding keeps core's exact rounding, since it decides the image.
@@ -39,7 +43,7 @@ generating = False
 def get_kernels():
     global kernels
     if kernels is None:
-        kernels = Kernels("int8_gemv", ("rotate", "gemv_i8", "gemv_bf16", "attn_decode", "attn_merge"))
+        kernels = Kernels("int8_gemv", ("rotate", "gemv_i8", "rotate_gemv_i8", "gemv_bf16", "attn_decode", "attn_merge"))
     return kernels
 
 
@@ -74,15 +78,29 @@ def _version(x):
         return None
 
 
+def _capturing(x):
+    return x.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+def cached_rotation(x, group):
+    """The rotation remembered for this same input x and group, or None."""
+    hit = _last_rotation
+    if hit is not None and hit[0] is x and hit[1] == _version(x) and hit[2] == group and hit[3] == _capturing(x):
+        return hit[4]
+    return None
+
+
+def remember_rotation(x, group, rotated):
+    global _last_rotation
+    _last_rotation = (x, _version(x), group, _capturing(x), rotated)
+
+
 def rotate_once(x, group):
     """rotate(x, group), or the rotation of the previous call when it had this same input."""
-    global _last_rotation
-    capturing = x.is_cuda and torch.cuda.is_current_stream_capturing()
-    hit = _last_rotation
-    if hit is not None and hit[0] is x and hit[1] == _version(x) and hit[2] == group and hit[3] == capturing:
-        return hit[4]
-    rotated = rotate(x, group)
-    _last_rotation = (x, _version(x), group, capturing, rotated)
+    rotated = cached_rotation(x, group)
+    if rotated is None:
+        rotated = rotate(x, group)
+        remember_rotation(x, group, rotated)
     return rotated
 
 
@@ -101,6 +119,19 @@ def gemv(x, weight, scale, bias=None):
     return out
 
 
+def rotate_gemv(x, group, weight, scale, bias=None, rotated=None):
+    """gemv(rotate(x, group), weight, scale, bias) as one launch, bit for bit: fp32 x of K values (contiguous), the
+    ConvRot of its K / group groups done by each workgroup of the GEMV in LDS; group one of FUSED_ROTATION_GROUPS.
+    rotated (fp32, K values, or None) receives rotate(x, group) as well. Returns fp32 (..., N)."""
+    if group not in FUSED_ROTATION_GROUPS:
+        raise ValueError(f"rotate_gemv rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
+    N, K = weight.shape
+    out = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
+    p = _lib.ptr
+    launch(get_kernels().rotate_gemv_i8, N // BLOCK_ROWS, 1, 256, [p(x), group, p(weight), p(scale), p(bias), p(out), p(rotated), N, K])
+    return out
+
+
 def linear_forward(module, N, K, weight_dtype, group, x, *args, **kwargs):
     """Int8 Linear.forward for text generation (int8_gemv.py:48-64): one token goes to the GEMV; several tokens of a
     generate() prefill with a large ConvRot group use a dequantized matmul; everything else keeps the layer's forward."""
@@ -109,9 +140,16 @@ def linear_forward(module, N, K, weight_dtype, group, x, *args, **kwargs):
         return type(module).forward(module, x, *args, **kwargs)
     x = x.contiguous()
     with quantized_weight(module, weight_dtype, x) as (weight, bias):
-        if group:
-            x = rotate_once(x, group)
         scale = weight._params.scale.to(device=x.device)
+        if group:
+            rotated = cached_rotation(x, group)
+            if rotated is None and single and group in FUSED_ROTATION_GROUPS and K <= FUSED_ROTATION_MAX_K:
+                # the first linear of this input rotates it inside its GEMV launch and keeps the rotation for the next
+                rotated = torch.empty_like(x)
+                out = rotate_gemv(x, group, weight._qdata, scale, bias, rotated)
+                remember_rotation(x, group, rotated)
+                return out
+            x = rotate_once(x, group) if rotated is None else rotated
         if not single:
             return F.linear(x, weight._qdata.to(x.dtype) * scale, bias)
         return gemv(x, weight._qdata, scale, bias)

@@ -110,6 +110,13 @@ int rda_rotate(const float* x, float* out, int rows, int group, void* stream);
  * x_half = 0: x, out fp32; x_half = 1: x, out fp16. K % 512 == 0, K <= 16384. */
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream);
 
+/* rotate followed by gemv_i8, int8_gemv.py:58-63 (int8_gemv.hip:31-85) -- linear_forward's single-token ConvRot
+ * linear -- as one launch: out (fp32) equals, bit for bit, rda_rotate of fp32 x in K / group groups of `group` (4, 16,
+ * 64 or 256) followed by rda_gemv_i8 of the rotated row. `rotated` (K floats, or NULL) receives that rotation too, for
+ * further linears of the same input. K % 512 == 0, K <= 16384; x is not modified. */
+int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* scale, const float* bias, float* out, float* rotated, int N, int K,
+                       void* stream);
+
 /* gemv_bf16, int8_gemv.py:97 (int8_gemv.hip:87-119): fp32 logits of a bf16 table. K % 256 == 0, N % 8 == 0. */
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream);
 

@@ -39,6 +39,43 @@ def test_ctypes_table_covers_header(built):
     assert set(_lib.SIGNATURES) == declared()
 
 
+def _params(text):
+    """Parameter types of a C parameter list, names dropped: "const float* x, int n" -> ["const float*", "int"]."""
+    text = " ".join(text.split())
+    if text in ("", "void"):
+        return []
+    types = []
+    for p in text.split(","):
+        p = re.sub(r"\s*\*\s*", "* ", p.strip()).strip()
+        types.append(re.sub(r"\s+\w+$", "", p).replace("* ", "*").strip())
+    return types
+
+
+def _signatures(text, pattern):
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return {m.group(2): (m.group(1), _params(m.group(3))) for m in re.finditer(pattern, text, flags=re.S)}
+
+
+def test_definitions_match_header_and_ctypes():
+    """Every entry point's definition in csrc/ has the parameter types include/rda.h declares, and the ctypes table
+    passes exactly those (a pointer as c_void_p, int, long, float), so a changed signature cannot go unnoticed."""
+    decl = _signatures(open(HEADER).read(), r"\b(int|size_t)\s+(rda_\w+)\s*\(([^)]*)\)\s*;")
+    csrc = os.path.join(ROOT, "comfyui-rdna2-attention_amd", "csrc")
+    defs = {}
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith(".hip"):
+            defs.update(_signatures(open(os.path.join(csrc, name)).read(), r"\b(int|size_t)\s+(rda_\w+)\s*\(([^)]*)\)\s*\{"))
+    assert set(decl) == declared() and set(defs) == set(decl)
+    ctype = {"int": ctypes.c_int, "long": ctypes.c_long, "float": ctypes.c_float, "size_t": ctypes.c_size_t}
+    for name, (ret, params) in decl.items():
+        assert defs[name] == (ret, params), f"{name}: header {ret} ({', '.join(params)}) vs definition {defs[name]}"
+        res, args = _lib.SIGNATURES[name]
+        assert res is ctype[ret], name
+        want = [ctypes.c_void_p if t.endswith("*") else ctype[t.replace("const ", "")] for t in params]
+        assert list(args) == want, f"{name}: ctypes {args} vs {want}"
+
+
 def test_library_loads_and_binds(built):
     lib = _lib.declare(ctypes.CDLL(built))
     assert lib.rda_version() == 1

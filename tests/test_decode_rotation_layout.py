@@ -1,0 +1,205 @@
+"""A CPU model of the ConvRot prologue of the fused decode GEMVs (rot_load / rot_to_lds in csrc/decode.hip).
+
+The model restates the kernel's integer index arithmetic and its float32 operations in their order, thread by thread,
+for the 512 threads of a workgroup: x is taken in sets of 16 consecutive values (set q = thread + 512 r); the H4 steps
+of stride 1 and 4 run on a set's registers; groups of 4 and 16 then write in reading order; larger groups write the
+sets in the padded natural layout (word v + 4 (v >> 4) + 16 (v >> 8)), read them back transposed (thread u takes the
+values 256 (u >> 4) + 16 i + (u & 15)), run the strides 16 and 64 in registers and, after every read, write in the
+padded reading order (f4 j of lane l in step s at (4 s + j) 77 + l + 4 (l >> 4)). It checks, over K and group:
+- every word written lies in the buffer the host sizes (rot_lds_bytes) and no two writes of a pass hit one word;
+- the kernel's closed-form addresses equal the layout functions they stand for;
+- the LDS banks (64 x 4 bytes) of each pass: a wave's transposed reads and reading-order writes touch 64 distinct
+  banks, and its 16-lane groups of 16-byte accesses (natural writes, product reads) 16 distinct 16-byte bank groups;
+- the buffer read back in reading order equals the oracle's rotation bit for bit.
+Planted mistakes (the transposed base off by one block, the stride-4 step skipped, the half step's lane order
+dropped, an even row length) fail it.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+NT, RO_ROW = 512, 77
+
+
+def nat_word(v):
+    return v + 4 * (v >> 4) + 16 * (v >> 8)
+
+
+def ro_f4(s, j, l, row=RO_ROW):
+    return (4 * s + j) * row + l + 4 * (l >> 4)
+
+
+def ro_of_value(v, steps, row=RO_ROW):
+    if v < steps * 1024:
+        return ro_f4(v >> 10, (v >> 2) & 3, (v >> 4) & 63, row)
+    t = v - steps * 1024
+    return ro_f4(steps, (t >> 2) & 1, t >> 3, row)
+
+
+def rot_lds_words(K):
+    rows = 4 * (K // 1024) + (2 if K % 1024 else 0)
+    return max(K + K // 4 + K // 16, 4 * rows * RO_ROW)
+
+
+def h4(a, b, c, d):
+    s = a + b + c + d  # float32, left to right
+    two = np.float32(2)
+    return s - two * d, s - two * c, s - two * b, s - two * a
+
+
+def check_banks(words, per_group, what):
+    """words[lane] for one instruction of one wave: each group of `per_group` lanes must hit distinct banks."""
+    for g0 in range(0, len(words), per_group):
+        grp = [w for w in words[g0:g0 + per_group] if w is not None]
+        if per_group == 64:
+            banks = [w % 64 for w in grp]
+        else:  # 16-byte accesses: 16 bank groups of 4 words
+            banks = [(w // 4) % 16 for w in grp]
+        assert len(set(banks)) == len(banks), f"{what}: bank conflict {sorted(banks)}"
+
+
+def rot_to_lds(x, K, group, mistake=None):
+    """The LDS buffer (float32 words) that rot_to_lds leaves for the products, and its reading-order read-back."""
+    steps, sets = K // 1024, K // 16
+    rs = 1 if sets <= NT else 2
+    row = 76 if mistake == "row" else RO_ROW
+    size = rot_lds_words(K)
+    xw = np.full(size, np.nan, np.float32)
+    norm = np.float32(1) / np.sqrt(np.float32(group))
+
+    def ro(v):
+        if mistake == "tail" and v >= steps * 1024:
+            return ro_f4(steps, 0, 0, row) + (v - steps * 1024) // 4
+        return ro_of_value(v, steps, row)
+
+    regs = {}
+    for t in range(NT):
+        for r in range(rs):
+            q = t + NT * r
+            src = 16 * (q if q < sets else 0)
+            regs[t, r] = [x[src + 4 * j:src + 4 * j + 4].astype(np.float32).copy() for j in range(4)]
+    for v in regs.values():
+        for j in range(4):
+            v[j] = np.array(h4(*v[j]), np.float32)  # stride 1
+        if group >= 16 and mistake != "skip4":
+            v[0], v[1], v[2], v[3] = h4(*v)  # stride 4
+    if group <= 16:
+        written = set()
+        for (t, r), v in regs.items():
+            q = t + NT * r
+            if q < sets:
+                for j in range(4):
+                    f = ro(16 * q + 4 * j)
+                    for e in range(4):
+                        assert 4 * f + e < size and 4 * f + e not in written
+                        written.add(4 * f + e)
+                        xw[4 * f + e] = v[j][e] * norm
+        return xw
+    # natural writes (f4s), with the kernel's closed form and its banks
+    written = set()
+    for r in range(rs):
+        for j in range(4):
+            for w0 in range(0, NT, 64):
+                lanes = []
+                for t in range(w0, w0 + 64):
+                    q = t + NT * r
+                    if q < sets:
+                        a = 20 * q + 16 * (q >> 4) + 4 * j
+                        assert a == nat_word(16 * q + 4 * j)
+                        lanes.append(a)
+                        for e in range(4):
+                            assert a + e < size and a + e not in written
+                            written.add(a + e)
+                            xw[a + e] = regs[t, r][j][e]
+                    else:
+                        lanes.append(None)
+                check_banks(lanes, 16, "natural write")
+    # transposed reads
+    y = {}
+    for r in range(rs):
+        for w0 in range(0, NT, 64):
+            for i in range(16):
+                lanes = []
+                for t in range(w0, w0 + 64):
+                    u = t + NT * r
+                    if u < sets:
+                        b = u >> 4
+                        base = 336 * b + (u & 15) + (336 if mistake == "base" else 0)
+                        a = base + 20 * i
+                        assert mistake == "base" or a == nat_word(256 * b + 16 * i + (u & 15))
+                        assert 0 <= a < size, "read outside the buffer"
+                        lanes.append(a)
+                        y.setdefault((t, r), [None] * 16)[i] = np.float32(xw[a])
+                    else:
+                        lanes.append(None)
+                check_banks(lanes, 64, "transposed read")
+    for yy in y.values():
+        for k in range(4):
+            yy[4 * k], yy[4 * k + 1], yy[4 * k + 2], yy[4 * k + 3] = h4(yy[4 * k], yy[4 * k + 1], yy[4 * k + 2], yy[4 * k + 3])
+        if group >= 256:
+            for m in range(4):
+                yy[m], yy[m + 4], yy[m + 8], yy[m + 12] = h4(yy[m], yy[m + 4], yy[m + 8], yy[m + 12])
+    # reading-order writes after every read
+    written = set()
+    for r in range(rs):
+        for w0 in range(0, NT, 64):
+            for i in range(16):
+                lanes = []
+                for t in range(w0, w0 + 64):
+                    u = t + NT * r
+                    if u < sets:
+                        b, p = u >> 4, u & 15
+                        if b < 4 * steps:
+                            a = 4 * ((4 * (b >> 2) + (p >> 2)) * row + 20 * (b & 3)) + (p & 3) + 4 * i
+                        else:
+                            a = 4 * ((4 * steps + ((p >> 2) & 1)) * row + 40 * (b - 4 * steps) + (p >> 3)) + (p & 3) + 8 * i + 16 * (i >> 3)
+                        val = 256 * b + 16 * i + p
+                        if mistake != "tail":
+                            assert a == 4 * ro(val & ~3) + (val & 3)
+                        else:
+                            a = 4 * ro(val & ~3) + (val & 3)
+                        assert 0 <= a < size and a not in written, "reading-order write outside the buffer or twice"
+                        written.add(a)
+                        lanes.append(a)
+                        xw[a] = y[t, r][i] * norm
+                    else:
+                        lanes.append(None)
+                if not any(256 * ((t + NT * r) >> 4) >= 1024 * steps for t in range(w0, w0 + 64) if t + NT * r < sets):
+                    check_banks(lanes, 64, "reading-order write")
+    return xw
+
+
+def read_back(xw, K, row=RO_ROW):
+    """x as the products read it: lane l's f4 j of step s from ro_f4(s, j, l); also checks their banks."""
+    steps = K // 1024
+    out = np.empty(K, np.float32)
+    for s in range(steps + (1 if K % 1024 else 0)):
+        for j in range(4 if s < steps else 2):
+            lanes = [4 * ro_f4(s, j, l, row) for l in range(64)]
+            check_banks(lanes, 16, "product read")
+            for l in range(64):
+                v = s * 1024 + (16 * l + 4 * j if s < steps else 8 * l + 4 * j)
+                out[v:v + 4] = xw[lanes[l]:lanes[l] + 4]
+    return out
+
+
+CASES = [(1024, 4), (1024, 16), (1024, 64), (1024, 256), (4096, 256), (4096, 64), (1536, 256), (512, 64), (512, 256),
+         (2560, 16), (12288, 256), (16384, 256), (9728, 256), (15872, 64), (8192, 256)]
+
+
+@pytest.mark.parametrize("K,group", CASES)
+def test_rotation_layout_matches_oracle(K, group):
+    x = np.random.default_rng(K + group).standard_normal(K).astype(np.float32)
+    got = read_back(rot_to_lds(x, K, group), K)
+    ref = oracle.rotate_f32(x.reshape(-1, group), group).reshape(-1)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("mistake,K,group", [("base", 4096, 256), ("skip4", 1024, 64), ("tail", 1536, 256), ("row", 4096, 256)])
+def test_model_catches_mistakes(mistake, K, group):
+    x = np.random.default_rng(7).standard_normal(K).astype(np.float32)
+    with pytest.raises(AssertionError):
+        xw = rot_to_lds(x, K, group, mistake=mistake)
+        ref = oracle.rotate_f32(x.reshape(-1, group), group).reshape(-1)
+        assert np.array_equal(read_back(xw, K, 76 if mistake == "row" else RO_ROW).view(np.uint32), ref.view(np.uint32))

@@ -58,6 +58,35 @@ def test_gemv_i8(dev, N, K, x_half):
     assert np.all(err <= bound), f"max err {err.max():.3e}"
 
 
+# split K (N <= 2048): (1024, 4096), (8, 1024), (2048, 8192), (1500, 2048), (1002, 16384); one row per wave: (4096, 4096),
+# (12288, 4096), (4096, 12288), (3000, 2048), and with a half step (K % 1024 == 512): (64, 512), (16, 1536), (4100, 9728)
+@pytest.mark.parametrize("N,K,group", [(1024, 4096, 256), (8, 1024, 4), (2048, 8192, 256), (1500, 2048, 16), (1002, 16384, 256), (4096, 4096, 256),
+                                       (12288, 4096, 64), (4096, 12288, 256), (3000, 2048, 64), (64, 512, 64), (16, 1536, 256), (4100, 9728, 256),
+                                       (4096, 16384, 16), (100, 4096, 4), (40, 15872, 256)])
+def test_rotate_gemv_i8_bit_exact(dev, N, K, group):
+    """rda_rotate_gemv_i8 (the ConvRot inside the GEMV launch) == rda_rotate then rda_gemv_i8, bit for bit; and the
+    rotation itself is the oracle's (rotate is bit-exact), the GEMV within its bound."""
+    print(f"rotate_gemv_i8 N={N} K={K} group={group}", flush=True)
+    x = torch.randn(1, K, generator=gen(K + group)).float()
+    w = int8_weights(N, K, seed=27)
+    s = channel_scales(N, seed=28)
+    bias = torch.randn(N, generator=gen(29)).float() if N in (64, 3000) else None
+    wd, sd, bd = w.to(dev), s.to(dev), None if bias is None else bias.to(dev)
+    xd = x.to(dev)
+    kept = torch.full_like(xd, float("nan"))
+    out = int8_gemv.rotate_gemv(xd, group, wd, sd, bd, kept)
+    rotated = int8_gemv.rotate(xd, group)
+    ref = int8_gemv.gemv(rotated, wd, sd, bd)
+    assert out.shape == (1, N) and out.dtype == torch.float32
+    assert torch.equal(xd.cpu(), x), "x was modified"
+    assert_same(out.cpu().numpy(), ref.cpu().numpy())
+    assert_same(kept.cpu().numpy(), rotated.cpu().numpy(), "stored rotation")
+    assert torch.equal(int8_gemv.rotate_gemv(xd, group, wd, sd, bd), out)  # without a rotation to store
+    xr = oracle.rotate_f32(x.numpy().reshape(-1, group), group).reshape(-1)
+    f64 = oracle.gemv_f64(xr, w.numpy(), s.numpy(), None if bias is None else bias.numpy())
+    assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - f64) <= gemv_bound(w.numpy(), xr, s.numpy(), False))
+
+
 @pytest.mark.parametrize("N,K", [(512, 1024), (64, 2560), (8, 256)])
 def test_gemv_bf16(dev, N, K):
     x = torch.randn(1, 1, K, generator=gen(20)).float()

@@ -41,7 +41,7 @@ def int8_layer():
     return layer
 
 
-@pytest.mark.parametrize("group", [0, 256, 1024])
+@pytest.mark.parametrize("group", [0, 64, 256, 1024])
 @pytest.mark.parametrize("N,K,bias", [(1024, 4096, False), (4096, 4096, True), (512, 12288, False)])
 def test_linear_forward_single_token(dev, monkeypatch, N, K, bias, group):
     print(f"linear_forward N={N} K={K} bias={bias} group={group}", flush=True)
@@ -61,34 +61,69 @@ def test_linear_forward_single_token(dev, monkeypatch, N, K, bias, group):
     assert np.all(err <= bound), f"max err {err.max():.3e}"
 
 
-def test_linear_forward_shares_one_rotation(dev, monkeypatch):
-    """q, k and v read one input: the first linear rotates it and the next two reuse that rotation (int8_gemv's
-    rotate_once); each output matches the oracle, and after an in-place write to the input the next call rotates
-    the new values."""
+def test_linear_forward_single_token_fuses_the_rotation(dev, monkeypatch):
+    """q, k and v read one input: the first single-token linear runs the ConvRot inside its GEMV launch
+    (rda_rotate_gemv_i8), which also stores the rotation; k and v reuse that stored rotation with the plain GEMV. Every
+    output equals rotate then gemv bit for bit, the stored rotation equals rotate's, and after an in-place write to
+    the input the next call rotates the new values."""
     K = 4096
-    layers, pairs, refs = [], {}, []
+    layers, pairs = [], {}
     for i, N in enumerate((4096, 1024, 1024)):
         w, s = int8_weights(N, K, seed=40 + i), channel_scales(N, seed=50 + i)
         layer = int8_layer()
         pairs[id(layer)] = (types.SimpleNamespace(_qdata=w.to(dev), _params=types.SimpleNamespace(scale=s.to(dev))), None)
-        layers.append((layer, N, w, s))
+        layers.append((layer, N, w.to(dev), s.to(dev)))
     stand_in_comfy(monkeypatch, pairs)
     int8_gemv.forget_rotation()
     x = torch.randn(1, 1, K, generator=gen(60)).float().to(dev)
+    rotated = int8_gemv.rotate(x, 256)
+    calls = []
+    fused = int8_gemv.rotate_gemv
+    monkeypatch.setattr(int8_gemv, "rotate_gemv", lambda *a, **k: calls.append(1) or fused(*a, **k))
+    for layer, N, w, s in layers:
+        out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+        assert torch.equal(out, int8_gemv.gemv(rotated, w, s))
+    assert len(calls) == 1, "k and v did not reuse the stored rotation"
+    assert torch.equal(int8_gemv._last_rotation[4], rotated)
+    x.mul_(-0.5)
+    layer, N, w, s = layers[0]
+    out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+    assert len(calls) == 2 and torch.equal(out, int8_gemv.gemv(int8_gemv.rotate(x, 256), w, s))
+    int8_gemv.forget_rotation()
+
+
+def test_linear_forward_prefill_shares_one_rotation(dev, monkeypatch):
+    """A generate() prefill (3 tokens, ConvRot group 1024): q, k and v read one input, the first linear rotates it and
+    the next two reuse that rotation (int8_gemv's rotate_once) for their dequantized matmuls; each output matches
+    the oracle, and after an in-place write to the input the next call rotates the new values. Bound: 1e-4 of
+    scale * sum_k |w x| (fp32 matmul of 4096 terms)."""
+    K, T, group = 4096, 3, 1024
+    layers, pairs = [], {}
+    for i, N in enumerate((4096, 1024, 1024)):
+        w, s = int8_weights(N, K, seed=40 + i), channel_scales(N, seed=50 + i)
+        layer = int8_layer()
+        # per-channel scales as a column, as the dequantized matmul broadcasts them over the (N, K) weight
+        pairs[id(layer)] = (types.SimpleNamespace(_qdata=w.to(dev), _params=types.SimpleNamespace(scale=s.view(N, 1).to(dev))), None)
+        layers.append((layer, N, w, s))
+    stand_in_comfy(monkeypatch, pairs)
+    monkeypatch.setattr(int8_gemv, "generating", True)
+    int8_gemv.forget_rotation()
+    x = torch.randn(1, T, K, generator=gen(60)).float().to(dev)
 
     def check(layer, N, w, s, out):
-        xr = oracle.rotate_f32(x.cpu().numpy().reshape(1, K), 256).reshape(-1)
-        ref = oracle.gemv_f64(xr, w.numpy(), s.numpy())
-        bound = 1e-5 * (np.abs(w.numpy().astype(np.float64)) @ np.abs(xr.astype(np.float64))) * np.abs(s.numpy()) + 1e-12
-        assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - ref) <= bound)
+        xr = oracle.rotate_f32(x.cpu().numpy().reshape(T, K), group).astype(np.float64)
+        wd = w.numpy().astype(np.float64)
+        ref = (xr @ wd.T) * s.numpy()
+        bound = 1e-4 * (np.abs(xr) @ np.abs(wd).T) * np.abs(s.numpy()) + 1e-12
+        assert np.all(np.abs(out.cpu().double().numpy().reshape(T, N) - ref) <= bound)
 
-    outs = [int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x) for layer, N, _, _ in layers]
+    outs = [int8_gemv.linear_forward(layer, N, K, torch.int8, group, x) for layer, N, _, _ in layers]
     rotated = int8_gemv._last_rotation[4]
     for (layer, N, w, s), out in zip(layers, outs):
         check(layer, N, w, s, out)
     x.mul_(-0.5)
     layer, N, w, s = layers[0]
-    out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+    out = int8_gemv.linear_forward(layer, N, K, torch.int8, group, x)
     assert int8_gemv._last_rotation[4] is not rotated
     check(layer, N, w, s, out)
     int8_gemv.forget_rotation()

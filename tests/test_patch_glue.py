@@ -466,3 +466,43 @@ def test_rotation_reused_by_consecutive_linears(monkeypatch):
     int8_gemv.generate(T())
     int8_gemv.rotate_once(x, 64)
     assert len(calls) == 7
+
+
+def test_single_token_linears_fuse_the_first_rotation(monkeypatch):
+    """linear_forward's single-token path (int8_gemv.py:58-63): the first linear of an input rotates it inside its GEMV
+    launch and keeps the rotation; the next linears of that input (k and v after q) run the plain GEMV on it; a new
+    input fuses again; K past FUSED_ROTATION_MAX_K, a group outside FUSED_ROTATION_GROUPS and no group take rotate then
+    GEMV, or the plain GEMV. Kernel calls are recorded by stand-ins (no GPU here)."""
+    cast_context(monkeypatch)
+    calls = []
+
+    def fused(x, group, w, s, b=None, rotated=None):
+        calls.append(("fused", group, w.shape[1]))
+        rotated.copy_(x * 2)
+        return torch.zeros(w.shape[0])
+
+    monkeypatch.setattr(int8_gemv, "rotate_gemv", fused)
+    monkeypatch.setattr(int8_gemv, "rotate", lambda x, group: calls.append(("rotate", group, x.shape[-1])) or x * 2)
+    monkeypatch.setattr(int8_gemv, "gemv", lambda x, w, s, b=None: calls.append(("gemv", float(x.sum()), w.shape[1])) or torch.zeros(w.shape[0]))
+
+    def layer(N, K):
+        m = types.SimpleNamespace(weight_function=None, bias_function=None)
+        m.qweight = types.SimpleNamespace(_qdata=torch.zeros(N, K, dtype=torch.int8), _params=types.SimpleNamespace(scale=torch.ones(N)))
+        return m
+
+    int8_gemv.forget_rotation()
+    x = torch.ones(1, 4096)
+    for N in (4096, 1024, 1024):
+        int8_gemv.linear_forward(layer(N, 4096), N, 4096, torch.int8, 256, x)
+    assert calls == [("fused", 256, 4096), ("gemv", 2 * 4096.0, 4096), ("gemv", 2 * 4096.0, 4096)]
+    calls.clear()
+    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 256, torch.ones(1, 4096))  # a new input
+    assert calls == [("fused", 256, 4096)]
+    calls.clear()
+    big = torch.ones(1, 12288)
+    int8_gemv.linear_forward(layer(64, 12288), 64, 12288, torch.int8, 256, big)  # K = 12288: rotate, then GEMV
+    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 1024, x)  # group 1024: not fused
+    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 0, x)  # no ConvRot
+    assert calls == [("rotate", 256, 12288), ("gemv", 2 * 12288.0, 12288), ("rotate", 1024, 4096), ("gemv", 2 * 4096.0, 4096),
+                     ("gemv", 4096.0, 4096)]
+    int8_gemv.forget_rotation()
