@@ -299,7 +299,7 @@ def w_decode_layer(torch, dev):
     111-113): hidden 4096, 32 query / 8 KV heads of 128, MLP 12288, KV cache length 2048 (fp32). Each of the seven
     int8 linears is int8_gemv.linear_forward's single-token path -- the ConvRot of its fp32 input (group 256) and the
     GEMV: the first linear of an input rotates it inside its GEMV launch and keeps the rotation, which k and v (after
-    q) and up (after gate) reuse; the down projection (K = 12288) rotates then runs the GEMV -- with a
+    q) and up (after gate) reuse -- with a
     stand-in for ComfyUI's quantized-weight context handing it the layer's int8 weight; attention is
     int8_gemv.attention_decode; the layer's own torch ops (norms, rope, silu * up, residual adds) are outside this
     path and not included. Replayed from a HIP graph, as a decode loop would, over enough weight and cache copies

@@ -177,9 +177,10 @@ __device__ __forceinline__ void rot_to_lds(f4 (&v)[RS][4], f4* xs, int K, int gr
 
 // out[n] = scale[n] * sum_k w[n, k] x[k] (+ bias[n]) (int8_gemv.hip:54-85). Each wave owns one row
 // and reads it in steps of 1024 values (16 per lane), plus a last half step of 512 (8 per lane) when
-// TAIL (K % 1024 == 512). x is fp32 or fp16; out has the dtype of x. One row per wave and 8 waves per
+// TAIL (K % 1024 == 512). x is fp32 or fp16; out has the dtype of x. One row per wave and NW = 8 waves per
 // block measured fastest on the decode shapes (K = 4096, N = 1024 .. 12288): more waves in flight per CU
-// beat more rows per wave, and larger blocks (which read x fewer times) did not gain.
+// beat more rows per wave, and larger blocks (which read x fewer times) did not gain. Rotated rows of more
+// than 8192 values (without a half step) take NW = 16, so that each thread holds one set of x.
 //
 // One memory round trip per launch: every load of the kernel is issued at the start, x and the row scale
 // first, then the G steps of the row (the host picks G >= K / 1024). Loads complete in issue order, so
@@ -190,28 +191,29 @@ __device__ __forceinline__ void rot_to_lds(f4 (&v)[RS][4], f4* xs, int K, int gr
 // x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the
 // f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
 // ROT: x (fp32) is first rotated in groups of `group` by the workgroup (rot_to_lds), bit for bit as rotate_kernel
-// would, so that one launch replaces rotate + GEMV; its loads go out before the weights' as well.
-template <int G, bool TAIL, bool XH, bool ROT>
-__global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
+// would, so that one launch replaces rotate + GEMV; its loads go out before the weights' as well; in ROT mode
+// the LDS copy is in rot_to_lds's padded reading order (ro_f4).
+template <int G, bool TAIL, bool XH, bool ROT, int NW>
+__global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(const void* __restrict__ xin, const int8_t* __restrict__ w, const float* __restrict__ scale,
                                                                  const float* __restrict__ bias, void* __restrict__ out, int N, int K, int group,
                                                                  float* __restrict__ rot_out) {
-    constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;  // float4s of x per thread: K / 4 <= 64 GI_WAVES XS
-    constexpr int RS = (64 * G + (TAIL ? 32 : 0) + GI_WAVES * 64 - 1) / (GI_WAVES * 64) < 2 ? 1 : 2;  // ROT: sets of 16 per thread, K <= 16384
+    constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + NW - 1) / NW;  // float4s of x per thread: K / 4 <= 64 NW XS
+    constexpr int RS = (64 * G + (TAIL ? 32 : 0) + NW * 64 - 1) / (NW * 64) < 2 ? 1 : 2;  // ROT: sets of 16 per thread, K <= 16384
     extern __shared__ f4 xs[];
     const int steps = K / 1024;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * GI_WAVES + wave;
+    const int row = blockIdx.x * NW + wave;
     const bool active = row < N;
     const int8_t* base = w + (size_t)(active ? row : 0) * K;
     typedef typename std::conditional<XH, h4v, f4>::type xv_t;
     xv_t xr[XS];
     f4 xq[RS][4];
     if constexpr (ROT) {
-        rot_load<GI_WAVES * 64, RS>((const float*)xin, K, xq);
+        rot_load<NW * 64, RS>((const float*)xin, K, xq);
     } else {
 #pragma unroll
         for (int j = 0; j < XS; j++) {
-            const int i = threadIdx.x + j * GI_WAVES * 64;
+            const int i = threadIdx.x + j * NW * 64;
             xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
         }
     }
@@ -228,11 +230,11 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_kernel(const void* __re
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (ROT) {
-        rot_to_lds<GI_WAVES * 64, RS>(xq, xs, K, group, steps, blockIdx.x == 0 ? rot_out : nullptr);
+        rot_to_lds<NW * 64, RS>(xq, xs, K, group, steps, blockIdx.x == 0 ? rot_out : nullptr);
     } else {
 #pragma unroll
         for (int j = 0; j < XS; j++) {
-            const int i = threadIdx.x + j * GI_WAVES * 64;
+            const int i = threadIdx.x + j * NW * 64;
             if (i < K / 4) {
                 f4 x;
                 if constexpr (XH) x = (f4){(float)xr[j][0], (float)xr[j][1], (float)xr[j][2], (float)xr[j][3]};
@@ -560,12 +562,15 @@ __global__ __launch_bounds__(HEAD) void attn_merge_kernel(const float* __restric
 
 template <int G, bool TAIL, bool XH, bool ROT>
 static int launch_gemv(const void* x, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out, void* stream) {
+    // rows past 8192 values with the rotation: 16 waves of one row each, so that a thread holds one set of x and the
+    // registers (114) leave a workgroup per CU; with a half step that shape would spill, and keeps 8 waves
+    constexpr int NW = ROT && G == 16 && !TAIL ? 16 : GI_WAVES;
     const size_t lds = ROT ? rot_lds_bytes(K) : (size_t)K * 4;
     if constexpr (ROT) {  // K > 12288: more than 64 KiB
         static std::atomic<size_t> done[RDA_MAX_DEVICES];
-        if (const int e = ensure_dynamic_lds((const void*)gemv_i8_kernel<G, TAIL, XH, ROT>, lds, done)) return e;
+        if (const int e = ensure_dynamic_lds((const void*)gemv_i8_kernel<G, TAIL, XH, ROT, NW>, lds, done)) return e;
     }
-    hipLaunchKernelGGL((gemv_i8_kernel<G, TAIL, XH, ROT>), dim3((N + GI_WAVES - 1) / GI_WAVES), dim3(GI_WAVES * 64), lds, (hipStream_t)stream, x,
+    hipLaunchKernelGGL((gemv_i8_kernel<G, TAIL, XH, ROT, NW>), dim3((N + NW - 1) / NW), dim3(NW * 64), lds, (hipStream_t)stream, x,
                        (const int8_t*)w, scale, bias, out, N, K, group, rot_out);
     return (int)hipGetLastError();
 }

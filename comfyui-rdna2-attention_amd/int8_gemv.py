@@ -31,9 +31,13 @@ GROUPS = 4  # query heads per KV head that patch() requires
 HEAD = 128
 FAST_DEQUANT_GROUP = 256  # Larger ConvRot groups make kitchen's dequantize fall back to a dense matmul.
 FUSED_ROTATION_GROUPS = (4, 16, 64, 256)  # ConvRot groups that rotate_gemv rotates inside the GEMV's launch
-# linear_forward fuses the rotation up to this K: past it the GEMV holds 16 weight steps per lane and the rotation's
-# registers leave one workgroup per CU (K = 12288: 16.3 us fused against 14.6 us for rotate then GEMV)
-FUSED_ROTATION_MAX_K = 8192
+
+
+def fuse_rotation(K):
+    """Whether linear_forward rotates inside the GEMV launch for rows of K values: up to 8192, and past it when K is a
+    multiple of 1024 (16-wave workgroups). Rows past 8192 with a half step of 512 keep 8-wave workgroups whose registers
+    leave one per CU, slower than rotate then GEMV."""
+    return K <= 8192 or K % 1024 == 0
 
 kernels = None
 # True inside generate(): prompt encoding keeps core's exact rounding, since it decides the image.
@@ -143,7 +147,7 @@ def linear_forward(module, N, K, weight_dtype, group, x, *args, **kwargs):
         scale = weight._params.scale.to(device=x.device)
         if group:
             rotated = cached_rotation(x, group)
-            if rotated is None and single and group in FUSED_ROTATION_GROUPS and K <= FUSED_ROTATION_MAX_K:
+            if rotated is None and single and group in FUSED_ROTATION_GROUPS and fuse_rotation(K):
                 # the first linear of this input rotates it inside its GEMV launch and keeps the rotation for the next
                 rotated = torch.empty_like(x)
                 out = rotate_gemv(x, group, weight._qdata, scale, bias, rotated)

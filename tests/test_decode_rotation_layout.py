@@ -1,7 +1,7 @@
 """A CPU model of the ConvRot prologue of the fused decode GEMVs (rot_load / rot_to_lds in csrc/decode.hip).
 
 The model restates the kernel's integer index arithmetic and its float32 operations in their order, thread by thread,
-for the 512 threads of a workgroup: x is taken in sets of 16 consecutive values (set q = thread + 512 r); the H4 steps
+for the 512 (or 1024) threads of a workgroup: x is taken in sets of 16 consecutive values (set q = thread + NT r); the H4 steps
 of stride 1 and 4 run on a set's registers; groups of 4 and 16 then write in reading order; larger groups write the
 sets in the padded natural layout (word v + 4 (v >> 4) + 16 (v >> 8)), read them back transposed (thread u takes the
 values 256 (u >> 4) + 16 i + (u & 15)), run the strides 16 and 64 in registers and, after every read, write in the
@@ -59,10 +59,10 @@ def check_banks(words, per_group, what):
         assert len(set(banks)) == len(banks), f"{what}: bank conflict {sorted(banks)}"
 
 
-def rot_to_lds(x, K, group, mistake=None):
+def rot_to_lds(x, K, group, mistake=None, NT=NT):
     """The LDS buffer (float32 words) that rot_to_lds leaves for the products, and its reading-order read-back."""
     steps, sets = K // 1024, K // 16
-    rs = 1 if sets <= NT else 2
+    rs = (sets + NT - 1) // NT
     row = 76 if mistake == "row" else RO_ROW
     size = rot_lds_words(K)
     xw = np.full(size, np.nan, np.float32)
@@ -188,10 +188,11 @@ CASES = [(1024, 4), (1024, 16), (1024, 64), (1024, 256), (4096, 256), (4096, 64)
          (2560, 16), (12288, 256), (16384, 256), (9728, 256), (15872, 64), (8192, 256)]
 
 
-@pytest.mark.parametrize("K,group", CASES)
-def test_rotation_layout_matches_oracle(K, group):
+@pytest.mark.parametrize("K,group,nt", [(K, g, 512) for K, g in CASES] + [(12288, 256, 1024), (16384, 64, 1024), (9216, 16, 1024)])
+def test_rotation_layout_matches_oracle(K, group, nt):
+    """512 threads (eight waves) everywhere; 1024 (sixteen waves) for rows past 8192 values."""
     x = np.random.default_rng(K + group).standard_normal(K).astype(np.float32)
-    got = read_back(rot_to_lds(x, K, group), K)
+    got = read_back(rot_to_lds(x, K, group, NT=nt), K)
     ref = oracle.rotate_f32(x.reshape(-1, group), group).reshape(-1)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 

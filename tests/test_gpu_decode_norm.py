@@ -59,10 +59,11 @@ def test_gemv_i8(dev, N, K, x_half):
 
 
 # split K (N <= 2048): (1024, 4096), (8, 1024), (2048, 8192), (1500, 2048), (1002, 16384); one row per wave: (4096, 4096),
-# (12288, 4096), (4096, 12288), (3000, 2048), and with a half step (K % 1024 == 512): (64, 512), (16, 1536), (4100, 9728)
+# (12288, 4096), (3000, 2048), and in 16-wave workgroups past K = 8192: (4096, 12288), (4096, 16384), (100, 9216); with a
+# half step (K % 1024 == 512): (64, 512), (16, 1536), (4100, 9728), (40, 15872)
 @pytest.mark.parametrize("N,K,group", [(1024, 4096, 256), (8, 1024, 4), (2048, 8192, 256), (1500, 2048, 16), (1002, 16384, 256), (4096, 4096, 256),
                                        (12288, 4096, 64), (4096, 12288, 256), (3000, 2048, 64), (64, 512, 64), (16, 1536, 256), (4100, 9728, 256),
-                                       (4096, 16384, 16), (100, 4096, 4), (40, 15872, 256)])
+                                       (4096, 16384, 16), (100, 4096, 4), (40, 15872, 256), (100, 9216, 64)])
 def test_rotate_gemv_i8_bit_exact(dev, N, K, group):
     """rda_rotate_gemv_i8 (the ConvRot inside the GEMV launch) == rda_rotate then rda_gemv_i8, bit for bit; and the
     rotation itself is the oracle's (rotate is bit-exact), the GEMV within its bound."""

@@ -471,8 +471,8 @@ def test_rotation_reused_by_consecutive_linears(monkeypatch):
 def test_single_token_linears_fuse_the_first_rotation(monkeypatch):
     """linear_forward's single-token path (int8_gemv.py:58-63): the first linear of an input rotates it inside its GEMV
     launch and keeps the rotation; the next linears of that input (k and v after q) run the plain GEMV on it; a new
-    input fuses again; K past FUSED_ROTATION_MAX_K, a group outside FUSED_ROTATION_GROUPS and no group take rotate then
-    GEMV, or the plain GEMV. Kernel calls are recorded by stand-ins (no GPU here)."""
+    input fuses again, K = 12288 too; K = 9728 (past 8192 with a half step), a group outside FUSED_ROTATION_GROUPS and
+    no group take rotate then GEMV, or the plain GEMV. Kernel calls are recorded by stand-ins (no GPU here)."""
     cast_context(monkeypatch)
     calls = []
 
@@ -499,10 +499,10 @@ def test_single_token_linears_fuse_the_first_rotation(monkeypatch):
     int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 256, torch.ones(1, 4096))  # a new input
     assert calls == [("fused", 256, 4096)]
     calls.clear()
-    big = torch.ones(1, 12288)
-    int8_gemv.linear_forward(layer(64, 12288), 64, 12288, torch.int8, 256, big)  # K = 12288: rotate, then GEMV
+    int8_gemv.linear_forward(layer(64, 12288), 64, 12288, torch.int8, 256, torch.ones(1, 12288))  # fused
+    int8_gemv.linear_forward(layer(64, 9728), 64, 9728, torch.int8, 256, torch.ones(1, 9728))  # rotate, then GEMV
     int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 1024, x)  # group 1024: not fused
     int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 0, x)  # no ConvRot
-    assert calls == [("rotate", 256, 12288), ("gemv", 2 * 12288.0, 12288), ("rotate", 1024, 4096), ("gemv", 2 * 4096.0, 4096),
-                     ("gemv", 4096.0, 4096)]
+    assert calls == [("fused", 256, 12288), ("rotate", 256, 9728), ("gemv", 2 * 9728.0, 9728), ("rotate", 1024, 4096),
+                     ("gemv", 2 * 4096.0, 4096), ("gemv", 4096.0, 4096)]
     int8_gemv.forget_rotation()
