@@ -670,6 +670,7 @@ int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* sc
                        void* stream) {
     if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
     if (group != 4 && group != 16 && group != 64 && group != 256) return RDA_ERR_INVALID;
+    if (((uintptr_t)x | (uintptr_t)rotated) & 15) return RDA_ERR_INVALID;  // read and written in 16-byte vectors
     return gemv_i8_dispatch<true>(x, 0, w, scale, bias, out, N, K, group, rotated, stream);
 }
 

@@ -129,6 +129,8 @@ def rotate_gemv(x, group, weight, scale, bias=None, rotated=None):
     rotated (fp32, K values, or None) receives rotate(x, group) as well. Returns fp32 (..., N)."""
     if group not in FUSED_ROTATION_GROUPS:
         raise ValueError(f"rotate_gemv rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
+    if x.data_ptr() % 16:  # the kernel reads x in 16-byte vectors
+        x = x.clone()
     N, K = weight.shape
     out = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
     p = _lib.ptr

@@ -113,7 +113,7 @@ int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, co
 /* rotate followed by gemv_i8, int8_gemv.py:58-63 (int8_gemv.hip:31-85) -- linear_forward's single-token ConvRot
  * linear -- as one launch: out (fp32) equals, bit for bit, rda_rotate of fp32 x in K / group groups of `group` (4, 16,
  * 64 or 256) followed by rda_gemv_i8 of the rotated row. `rotated` (K floats, or NULL) receives that rotation too, for
- * further linears of the same input. K % 512 == 0, K <= 16384; x is not modified. */
+ * further linears of the same input. K % 512 == 0, K <= 16384; x and rotated 16-byte aligned; x is not modified. */
 int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* scale, const float* bias, float* out, float* rotated, int N, int K,
                        void* stream);
 

@@ -88,6 +88,19 @@ def test_rotate_gemv_i8_bit_exact(dev, N, K, group):
     assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - f64) <= gemv_bound(w.numpy(), xr, s.numpy(), False))
 
 
+def test_rotate_gemv_unaligned_view(dev):
+    """An input view 4 bytes into its storage (taken through a 16-byte aligned copy): the same outputs and stored
+    rotation as rotate then gemv of the view."""
+    base = torch.randn(1 + 4096, generator=gen(43)).float().to(dev)
+    x = base[1:].view(1, 4096)
+    assert x.data_ptr() % 16 != 0
+    w, s = int8_weights(1024, 4096, seed=44).to(dev), channel_scales(1024, seed=45).to(dev)
+    kept = torch.empty(1, 4096, device=dev)
+    out = int8_gemv.rotate_gemv(x, 256, w, s, None, kept)
+    rotated = int8_gemv.rotate(x, 256)
+    assert torch.equal(out, int8_gemv.gemv(rotated, w, s)) and torch.equal(kept, rotated)
+
+
 @pytest.mark.parametrize("N,K", [(512, 1024), (64, 2560), (8, 256)])
 def test_gemv_bf16(dev, N, K):
     x = torch.randn(1, 1, K, generator=gen(20)).float()
