@@ -660,6 +660,7 @@ int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
 // x_half: 0 for fp32 x and out, 1 for fp16 x and out.
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream) {
     if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
+    if ((uintptr_t)x & 15) return RDA_ERR_INVALID;  // read in 16-byte vectors
     return gemv_i8_dispatch<false>(x, x_half, w, scale, bias, out, N, K, 0, nullptr, stream);
 }
 

@@ -116,6 +116,8 @@ def forget_rotation():
 def gemv(x, weight, scale, bias=None):
     """out[n] = scale[n] * dot(weight[n], x) (+ bias[n]) for one row x (K values, fp32 or fp16; the output has its dtype),
     weight (N, K) int8, scale (N,) fp32, bias (N,) fp32 or None."""
+    if x.data_ptr() % 16:  # the kernels read x in 16-byte vectors
+        x = x.clone()
     N, K = weight.shape
     out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
     p = _lib.ptr

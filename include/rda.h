@@ -107,7 +107,7 @@ int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, 
 int rda_rotate(const float* x, float* out, int rows, int group, void* stream);
 
 /* gemv_i8, int8_gemv.py:60-63 (int8_gemv.hip:54-85): out[n] = scale[n] * dot(w[n], x) (+ bias[n]).
- * x_half = 0: x, out fp32; x_half = 1: x, out fp16. K % 512 == 0, K <= 16384. */
+ * x_half = 0: x, out fp32; x_half = 1: x, out fp16. K % 512 == 0, K <= 16384; x 16-byte aligned. */
 int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, void* stream);
 
 /* rotate followed by gemv_i8, int8_gemv.py:58-63 (int8_gemv.hip:31-85) -- linear_forward's single-token ConvRot

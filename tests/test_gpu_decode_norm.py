@@ -88,6 +88,21 @@ def test_rotate_gemv_i8_bit_exact(dev, N, K, group):
     assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - f64) <= gemv_bound(w.numpy(), xr, s.numpy(), False))
 
 
+@pytest.mark.parametrize("half", [False, True])
+def test_gemv_unaligned_view(dev, half):
+    """An input view one element into its storage (taken through an aligned copy): within the bound of the others."""
+    base = torch.randn(1 + 4096, generator=gen(46))
+    base = (base.half() if half else base.float()).to(dev)
+    x = base[1:].view(1, 4096)
+    assert x.data_ptr() % 16 != 0
+    w, s = int8_weights(4096, 4096, seed=47), channel_scales(4096, seed=48)
+    out = int8_gemv.gemv(x, w.to(dev), s.to(dev))
+    xf = x.float().cpu().numpy().reshape(-1)
+    ref = oracle.gemv_f64(xf, w.numpy(), s.numpy())
+    bound = gemv_bound(w.numpy(), xf, s.numpy(), half) + (np.abs(ref) * 2.0 ** -10 if half else 0)
+    assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - ref) <= bound)
+
+
 def test_rotate_gemv_unaligned_view(dev):
     """An input view 4 bytes into its storage (taken through a 16-byte aligned copy): the same outputs and stored
     rotation as rotate then gemv of the view."""
