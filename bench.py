@@ -354,7 +354,7 @@ def w_decode_layer(torch, dev):
         lin(mods, "up", h)
         return lin(mods, "down", gate)
 
-    act = 4 * (D * 7 + Hkv * 128 * 2 + F * 4)  # fp32 inputs read (4 rotations, 7 GEMVs) and outputs written, roughly
+    act = 4 * (D * 7 + Hkv * 128 * 2 + F * 4)  # fp32 inputs read, rotations kept and outputs written, roughly
     work = weights_bytes + 4 * sum(n for n, _ in shapes.values()) + kv_bytes + act
     return step, copies, work, "hbm", graph_timed
 
