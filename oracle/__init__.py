@@ -329,18 +329,26 @@ def attention_i8qk_f64(q, k, v, scale):
     return (p @ v) / p.sum(-1, keepdims=True)
 
 
-def attention_faithful(q, k, v, scale, block=16, threshold=8.0):
-    """The reference's fused loop (hip_attention.hip:280-373) restated per query row in fp32:
-    scores in fp32, log2-domain online softmax with the lazy rescale (only when the block maximum passes
-    m + threshold), p = exp2(s * scale_log2 - m), l summed from the fp32 p, P rounded to fp16 for PV,
-    out = fp16(o * (1 / l)). Exponentials in float64 rounded to fp32 (the hardware's exp2 is not
-    reproducible, so this restatement is tolerance-level, not bit-level)."""
+def attention_faithful(q, k, v, scale, block=16, threshold=8.0, wave=32, stats=False):
+    """The reference's fused loop (hip_attention.hip:280-373) restated per query row in fp32.
+
+    Query rows run in waves of `wave` consecutive rows (hip_attention.hip:284-287; the padding lanes of a last,
+    partial wave repeat its last row, so they never change the vote). Per block of 16 keys: scores in fp32,
+    mx = fp32(max_j s_j) * scale_log2; when ANY row of the wave has mx > m + threshold, EVERY row of that wave
+    moves to m' = max(m, mx) and scales l and o by exp2(m - m') (hip_attention.hip:334-340); then
+    p = exp2(fp32(fma(s, scale_log2, -m))), l += p0 + p1 over the pairs in order, P rounded to fp16 for PV, and
+    out = fp16(o * (1 / l)). Exponentials in float64 rounded to fp32 (the hardware's exp2 is not reproducible, so
+    this restatement is tolerance-level, not bit-level). With stats=True also returns each row's final running
+    maximum m and sum l, shape (B, H, Lq)."""
     q, k, v = (np.asarray(t, np.float16) for t in (q, k, v))
     B, H, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     rep = H // Hkv
     scale_log2 = np.float32(scale * math.log2(math.e))
+    waves = np.arange(Lq) // wave
     out = np.empty((B, H, Lq, D), np.float16)
+    m_out = np.empty((B, H, Lq), np.float32)
+    l_out = np.empty((B, H, Lq), np.float32)
     for b in range(B):
         for h in range(H):
             kk = k[b, h // rep].astype(np.float32)
@@ -351,17 +359,22 @@ def attention_faithful(q, k, v, scale, block=16, threshold=8.0):
             o = np.zeros((Lq, D), np.float32)
             for g in range(0, Lk, block):
                 s = (qq.astype(np.float64) @ kk[g:g + block].astype(np.float64).T).astype(np.float32)
-                mx = s.max(1) * scale_log2
-                up = mx > m + np.float32(threshold)
+                mx = (s.max(1) * scale_log2).astype(np.float32)
+                vote = np.bincount(waves, weights=(mx > m + np.float32(threshold)).astype(np.float64)) > 0
+                up = vote[waves]
                 if up.any():
                     mn = np.maximum(m, mx)
-                    alpha = np.where(up, np.exp2((m - mn).astype(np.float64)).astype(np.float32), np.float32(1))
+                    alpha = np.where(up, np.exp2((m.astype(np.float64) - mn)).astype(np.float32), np.float32(1))
                     m = np.where(up, mn, m).astype(np.float32)
                     l = (l * alpha).astype(np.float32)
                     o = (o * alpha[:, None]).astype(np.float32)
-                p = np.exp2((s.astype(np.float64) * float(scale_log2) - m[:, None])).astype(np.float32)
-                l = (l + p.sum(1, dtype=np.float32)).astype(np.float32)
+                arg = (s.astype(np.float64) * float(scale_log2) - m[:, None].astype(np.float64)).astype(np.float32)
+                p = np.exp2(arg.astype(np.float64)).astype(np.float32)
+                for j in range(0, p.shape[1] - 1, 2):
+                    l = (l + (p[:, j] + p[:, j + 1]).astype(np.float32)).astype(np.float32)
+                if p.shape[1] % 2:
+                    l = (l + p[:, -1]).astype(np.float32)
                 o = (o + (p.astype(np.float16).astype(np.float64) @ vv[g:g + block].astype(np.float64))).astype(np.float32)
             out[b, h] = (o * (np.float32(1) / l)[:, None]).astype(np.float16)
-    return out
-
+            m_out[b, h], l_out[b, h] = m, l
+    return (out, m_out, l_out) if stats else out

@@ -24,6 +24,17 @@ What fixes each function, independently of the oracle's own formula:
 * modulate (int8_gemm.hip:140-143): r16(r16(r16(x rstd (w + 1)) s) + t): the first rounding is the correctly
   rounded float64 product (2^-19 margin), the second is exact fp16 of an exact product, the last fp16 of the
   IEEE float32 sum.
+* GEMM epilogue (int8_gemm.hip:382-383): y = ((float)acc * as) * ws, left to right, each step one IEEE fp32
+  rounding, then + bias and fp16. Evaluated in exact rationals with a rounding to fp32 after every operation.
+  The accumulators are chosen so that y lands within an fp32 ulp of an fp16 rounding midpoint, where the
+  association acc * (as * ws) gives another fp16 result; the check counts those inputs.
+* gated residual (int8_gemm.hip:394-400): C = fp16(R + fp16(G[m / L] * y)), contraction off: exact rationals,
+  with the inner fp16 rounding, against inputs where dropping it changes C.
+* RoPE (rms_norm.hip:55-57): a = fp16(fma(m1, x1, fp32(m0 x0))), c likewise with m2, m3: exact rationals, with
+  rotation matrices built so that the exact value lies near an fp16 midpoint, where evaluating with two separate
+  fp32 roundings, or in one exact step, gives another result.
+* W4A8 epilogue (no reference counterpart): y = fma((float)p_g, gs[n][g], y) over the groups in order, then
+  fp16(y * as (+ bias)): exact rationals with one fp32 rounding per fma and per operation.
 """
 import ctypes
 import math
@@ -35,7 +46,7 @@ import oracle
 
 
 def _ptr(a):
-    return a.ctypes.data_as(ctypes.c_void_p)
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
 def _rhe(fr):
@@ -291,6 +302,198 @@ def modulate_failures(L):
     return bad
 
 
+# ------------------------------------------------------------------- exact binary rounding (no numpy floats) ---
+
+def _round_binary(fr, p, emin, emax):
+    """fr rounded to the nearest binary float with p significant bits, normal exponents emin..emax and subnormals
+    below 2^emin, ties to even; magnitudes that round to 2^(emax + 1) or beyond become +-inf. Exact arithmetic."""
+    if fr == 0:
+        return Fraction(0)
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    elif Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp = Fraction(2) ** (max(e, emin) - p + 1)
+    r = _rhe(a / ulp) * ulp
+    if r >= Fraction(2) ** (emax + 1):
+        return math.inf if fr > 0 else -math.inf
+    return r if fr > 0 else -r
+
+
+def _r32(fr):
+    return _round_binary(fr, 24, -126, 127)
+
+
+def _r16(fr):
+    return _round_binary(fr, 11, -14, 15)
+
+
+def _fr(v):
+    return Fraction(float(v))
+
+
+def _as_f64(frs):
+    return np.array([float(v) for v in frs], np.float64)
+
+
+def _epilogue(L, acc, a_s, w_s, bias=None, R=None, G=None, Lg=1):
+    acc = np.ascontiguousarray(acc, np.int32)
+    M, N = acc.shape
+    out = np.empty((M, N), np.uint16)
+    a_s = np.ascontiguousarray(a_s, np.float32)
+    w_s = np.ascontiguousarray(w_s, np.float32)
+    args = [None if t is None else np.ascontiguousarray(t, np.float16) for t in (bias, R, G)]
+    L.orc_gemm_epilogue(M, N, _ptr(acc), _ptr(a_s), _ptr(w_s), *[_ptr(t) for t in args], Lg, _ptr(out))
+    return out.view(np.float16).astype(np.float64)
+
+
+def _midpoint_accumulators(rng, a_s, w_s, lo, hi, offset=None):
+    """acc[m, n] = the integer nearest (mid - offset[n]) / (as[m] ws[n]) for a random fp16 rounding midpoint mid in
+    [lo, hi]: with |acc| >= 2^23 the exact product plus the offset lies within about an fp32 ulp of the midpoint."""
+    grid = _fp16_grid(lo, hi)
+    M, N = a_s.size, w_s.size
+    h = grid[rng.integers(0, grid.size - 1, (M, N))]
+    up = np.nextafter(h.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+    mid = (h + up) / 2 * np.where(rng.random((M, N)) < 0.5, -1, 1)
+    if offset is not None:
+        mid = mid - np.asarray(offset, np.float64)[None]
+    acc = np.rint(mid / (a_s.astype(np.float64)[:, None] * w_s.astype(np.float64)[None]))
+    assert np.abs(acc).max() < 2 ** 31 and np.abs(acc).min() >= 2 ** 23
+    return acc.astype(np.int32)
+
+
+def epilogue_failures(L):
+    """((float)acc * as) * ws (+ bias) -> fp16, left to right."""
+    bad = []
+    rng = np.random.default_rng(31)
+    M, N = 48, 64
+    a_s = rng.uniform(2e-5, 1e-4, M).astype(np.float32)
+    w_s = rng.uniform(1e-3, 3e-3, N).astype(np.float32)
+    bias = rng.uniform(-2, 2, N).astype(np.float16)
+    for with_bias in (False, True):
+        acc = _midpoint_accumulators(rng, a_s, w_s, 6.0, 16.0, bias.astype(np.float64) if with_bias else None)
+        got = _epilogue(L, acc, a_s, w_s, bias if with_bias else None)
+        expect, other = [], 0
+        for m in range(M):
+            for n in range(N):
+                a, x, w = _r32(Fraction(int(acc[m, n]))), _fr(a_s[m]), _fr(w_s[n])
+                y = _r32(_r32(a * x) * w)
+                y2 = _r32(a * _r32(x * w))
+                if with_bias:
+                    y, y2 = _r32(y + _fr(bias[n])), _r32(y2 + _fr(bias[n]))
+                expect.append(_r16(y))
+                other += _r16(y2) != _r16(y)
+        expect = _as_f64(expect).reshape(M, N)
+        tag = "epilogue with bias" if with_bias else "epilogue"
+        if not np.array_equal(got, expect):
+            bad.append(f"{tag}: {int((got != expect).sum())} of {M * N} outputs differ from the left-to-right fp32 chain")
+        if other < M * N // 50:
+            bad.append(f"{tag}: only {other} inputs tell acc * (as * ws) apart")
+    return bad
+
+
+def gated_residual_failures(L):
+    """C = fp16(R + fp16(G[m / L] * y)) after the epilogue, with L tokens per gate row."""
+    bad = []
+    rng = np.random.default_rng(37)
+    M, N, Lg = 32, 64, 4
+    acc = rng.integers(-2 ** 22, 2 ** 22, (M, N)).astype(np.int32)
+    a_s = rng.uniform(1e-3, 1e-2, M).astype(np.float32)
+    w_s = rng.uniform(1e-3, 3e-3, N).astype(np.float32)
+    y = _epilogue(L, acc, a_s, w_s)
+    R = (rng.standard_normal((M, N)) * np.abs(y) * 2).astype(np.float16)
+    G = (rng.standard_normal((M // Lg, N)) * 2).astype(np.float16)
+    got = _epilogue(L, acc, a_s, w_s, R=R, G=G, Lg=Lg)
+    expect, single = [], 0
+    for m in range(M):
+        for n in range(N):
+            r, g, yv = _fr(R[m, n]), _fr(G[m // Lg, n]), Fraction(float(y[m, n]))
+            c = _r16(_r32(r + _r16(_r32(g * yv))))
+            expect.append(c)
+            single += _r16(_r32(r + _r32(g * yv))) != c
+    expect = _as_f64(expect).reshape(M, N)
+    if not np.array_equal(got, expect):
+        bad.append(f"gated residual: {int((got != expect).sum())} of {M * N} outputs differ")
+    if single < M * N // 50:
+        bad.append(f"gated residual: only {single} inputs tell a single rounding apart")
+    return bad
+
+
+def rope_failures(L):
+    """rms_norm_rope's rotation of each (x0, x1) pair of the normalised row."""
+    bad = []
+    rng = np.random.default_rng(41)
+    Lr, D = 24, 128
+    x = rng.standard_normal((Lr, D)).astype(np.float16)
+    w = (rng.standard_normal(D) * 0.1).astype(np.float32)
+
+    def norm(freqs):
+        y = np.empty((Lr, D), np.uint16)
+        L.orc_rms_norm(1, 1, Lr, D, _ptr(x), Lr * D, Lr * D, D, _ptr(w), np.float32(1e-6), _ptr(freqs), 0, _ptr(y))
+        return y.view(np.float16).astype(np.float64)
+
+    y = norm(None)
+    grid = _fp16_grid(0.25, 8.0)
+    f = rng.standard_normal((Lr, D // 2, 4)).astype(np.float32)
+    for l in range(Lr):
+        for p in range(D // 2):
+            x0, x1 = y[l, 2 * p], y[l, 2 * p + 1]
+            if x1 == 0:
+                continue
+            for i in (0, 2):  # second entry of each matrix row chosen so the row's result sits near a midpoint
+                h = grid[rng.integers(0, grid.size - 1)]
+                mid = (h + float(np.nextafter(np.float16(h), np.float16(np.inf)))) / 2 * (1 if rng.random() < .5 else -1)
+                f[l, p, i + 1] = np.float32((mid - float(f[l, p, i]) * x0) / x1)
+    got = norm(f)
+    expect, sep, once = [], 0, 0
+    for l in range(Lr):
+        for p in range(D // 2):
+            x0, x1 = Fraction(float(y[l, 2 * p])), Fraction(float(y[l, 2 * p + 1]))
+            for i in (0, 2):
+                m0, m1 = _fr(f[l, p, i]), _fr(f[l, p, i + 1])
+                v = _r16(_r32(m1 * x1 + _r32(m0 * x0)))
+                expect.append(v)
+                sep += _r16(_r32(_r32(m1 * x1) + _r32(m0 * x0))) != v
+                once += _r16(m1 * x1 + m0 * x0) != v
+    expect = _as_f64(expect).reshape(Lr, D)
+    if not np.array_equal(got, expect):
+        bad.append(f"rope: {int((got != expect).sum())} of {Lr * D} outputs differ from fp16(fma(m1, x1, fp32(m0 x0)))")
+    if sep < Lr * D // 50 or once < Lr * D // 50:
+        bad.append(f"rope: only {sep} / {once} inputs tell separate roundings / one exact step apart")
+    return bad
+
+
+def w4a8_epilogue_failures(L):
+    """y = fma((float)p_g, gs[n][g], y) in group order, then fp16(y * as (+ bias))."""
+    bad = []
+    rng = np.random.default_rng(43)
+    Gs, M, N = 6, 8, 32
+    parts = rng.integers(-2 ** 18, 2 ** 18, (Gs, M, N)).astype(np.int32)
+    a_s = rng.uniform(1e-4, 1e-2, M).astype(np.float32)
+    gs = rng.uniform(5e-3, 2e-2, (N, Gs)).astype(np.float16)
+    bias = rng.standard_normal(N).astype(np.float16)
+    for with_bias in (False, True):
+        out = np.empty((M, N), np.uint16)
+        L.orc_w4a8_epilogue(M, N, Gs, _ptr(parts), _ptr(a_s), _ptr(gs), _ptr(bias) if with_bias else None, _ptr(out))
+        got = out.view(np.float16).astype(np.float64)
+        expect = []
+        for m in range(M):
+            for n in range(N):
+                yv = Fraction(0)
+                for g in range(Gs):
+                    yv = _r32(Fraction(int(parts[g, m, n])) * _fr(gs[n, g]) + yv)
+                t = _r32(yv * _fr(a_s[m]))
+                if with_bias:
+                    t = _r32(t + _fr(bias[n]))
+                expect.append(_r16(t))
+        expect = _as_f64(expect).reshape(M, N)
+        if not np.array_equal(got, expect):
+            bad.append(f"w4a8 epilogue{' with bias' if with_bias else ''}: {int((got != expect).sum())} outputs differ")
+    return bad
+
+
 CHECKS = {
     "rint": rint_failures,
     "i4": i4_failures,
@@ -299,4 +502,8 @@ CHECKS = {
     "sigmoid_gate": sigmoid_gate_failures,
     "situ": situ_failures,
     "modulate": modulate_failures,
+    "epilogue": epilogue_failures,
+    "gated_residual": gated_residual_failures,
+    "rope": rope_failures,
+    "w4a8_epilogue": w4a8_epilogue_failures,
 }

@@ -69,7 +69,7 @@ def test_attention_zero_query_rows(dev, int8_qk):
 
 
 def test_attention_matches_reference_loop(dev):
-    """Tighter: the reference's own loop restated in fp32 (lazy rescale, fp16 P) agrees with the kernel."""
+    """Tighter: the reference's own loop restated in fp32 (wave-voted lazy rescale, fp16 P) agrees with the kernel."""
     q, k, v = qkv(1, 2, 2, 256, 700, seed=3)
     out = torch.empty(1, 2, 256, 128, dtype=torch.float16, device=dev)
     hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, 128 ** -0.5)

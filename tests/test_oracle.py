@@ -256,6 +256,32 @@ def test_attention_restatements_agree():
     assert np.allclose(ref[0, 1, 3], row, atol=1e-12)
 
 
+def test_attention_faithful_rescale_is_voted_per_wave():
+    """hip_attention.hip:334-340: a wave rescales when ANY of its rows' block maximum passes m + 8, and then every row
+    moves to max(m, mx). Row 0's scores rise by 16 (log2 units) per block, so it votes every block; rows 1-3 have flat
+    scores. Voted with row 0 (one wave) they end at their own overall maximum; in waves of one row they keep their
+    first block's maximum. Either way the output stays the softmax of float64."""
+    D, Lk, scale = 128, 64, 128 ** -0.5
+    sl2 = scale * math.log2(math.e)
+    q = np.zeros((1, 1, 4, D), np.float16)
+    q[0, 0, :, 0] = 1
+    k = np.zeros((1, 1, Lk, D), np.float16)
+    k[0, 0, :, 0] = (np.arange(Lk) // 16 * 16 / sl2).astype(np.float16)  # row 0: block maxima 0, 16, 32, 48
+    q[0, 0, 1:, 0] = 0
+    q[0, 0, 1:, 1] = 1
+    k[0, 0, :, 1] = (rng.uniform(0, 4, Lk) / sl2).astype(np.float16)  # rows 1-3: scores below 4 everywhere
+    v = rng.standard_normal((1, 1, Lk, D)).astype(np.float16)
+    ref = oracle.attention_f64(q, k, v, scale)
+    s1 = (q[0, 0, 1].astype(np.float64) @ k[0, 0].astype(np.float64).T).astype(np.float32)
+    one_wave, m1, _ = oracle.attention_faithful(q, k, v, scale, stats=True)
+    per_row, m2, _ = oracle.attention_faithful(q, k, v, scale, wave=1, stats=True)
+    assert m1[0, 0, 1] == np.float32(s1.max() * np.float32(sl2))
+    assert m2[0, 0, 1] == np.float32(s1[:16].max() * np.float32(sl2))
+    assert m1[0, 0, 0] == m2[0, 0, 0]
+    for o in (one_wave, per_row):
+        assert np.abs(o.astype(np.float64) - ref).max() < 2e-3
+
+
 def test_decode_attention_closed_form():
     q = rng.standard_normal((1, 1, 8, 128)).astype(np.float32)
     k = rng.standard_normal((1, 50, 2, 128)).astype(np.float32)

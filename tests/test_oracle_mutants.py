@@ -35,6 +35,21 @@ MUTANTS = [
      "float sigmoid = r16(1.0f / (1.0f + orc_exp2f(-1.442695041f * gate)));"),
     ("modulate_middle_rounding_dropped", "modulate", "return r16(r16(r16(x * rstd * (w + 1.0f)) * s) + t);",
      "return r16(r16(x * rstd * (w + 1.0f)) * s + t);"),
+    ("epilogue_scales_multiplied_first", "epilogue", "float y = (float)acc[(size_t)m * N + n] * as[m] * ws[n];",
+     "float y = (float)acc[(size_t)m * N + n] * (as[m] * ws[n]);"),
+    ("epilogue_bias_fused", "epilogue", "if (bias) y = y + h2f(bias[n]);",
+     "if (bias) y = fmaf((float)acc[(size_t)m * N + n] * as[m], ws[n], h2f(bias[n]));"),
+    ("residual_inner_rounding_dropped", "gated_residual", "h = f2h(res + r16(gate * h2f(h)));",
+     "h = f2h(res + gate * h2f(h));"),
+    ("residual_gate_row_index", "gated_residual", "gate = h2f(G[(size_t)(m / L) * N + n]);",
+     "gate = h2f(G[(size_t)(m % L) * N + n]);"),
+    ("rope_in_double", "rope", "float a = fmaf(m[1], x1, m[0] * x0), c = fmaf(m[3], x1, m[2] * x0);",
+     "float a = (float)((double)m[1] * x1 + (double)m[0] * x0), c = (float)((double)m[3] * x1 + (double)m[2] * x0);"),
+    ("rope_separate_roundings", "rope", "float a = fmaf(m[1], x1, m[0] * x0), c = fmaf(m[3], x1, m[2] * x0);",
+     "float a = m[1] * x1 + m[0] * x0, c = m[3] * x1 + m[2] * x0;"),
+    ("rope_matrix_transposed", "rope", "float a = fmaf(m[1], x1, m[0] * x0), c = fmaf(m[3], x1, m[2] * x0);",
+     "float a = fmaf(m[2], x1, m[0] * x0), c = fmaf(m[3], x1, m[1] * x0);"),
+    ("w4a8_scale_before_sum", "w4a8_epilogue", "float t = y * as[m];", "float t = r16(y) * as[m];"),
 ]
 
 
