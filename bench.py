@@ -298,9 +298,9 @@ def w_decode_layer(torch, dev):
     """One token through one Qwen3-8B-shaped layer as int8_gemv's patched forwards run it (int8_gemv.py:48-64,
     111-113): hidden 4096, 32 query / 8 KV heads of 128, MLP 12288, KV cache length 2048 (fp32). Each of the seven
     int8 linears is int8_gemv.linear_forward's single-token path -- the ConvRot of its fp32 input (group 256) and the
-    GEMV: the first linear of an input rotates it inside its GEMV launch and keeps the rotation, which k and v (after
-    q) and up (after gate) reuse -- with a
-    stand-in for ComfyUI's quantized-weight context handing it the layer's int8 weight; attention is
+    GEMV, in one launch -- with q, k, v and gate, up registered as siblings as int8_gemv.patch() registers them, so
+    that each set runs as one launch over its shared input; a stand-in for ComfyUI's quantized-weight context hands
+    them the layer's int8 weights; attention is
     int8_gemv.attention_decode; the layer's own torch ops (norms, rope, silu * up, residual adds) are outside this
     path and not included. Replayed from a HIP graph, as a decode loop would, over enough weight and cache copies
     that the Infinity Cache cannot serve them. Bytes: the int8 weights, their scales, the K/V cache and the
@@ -334,6 +334,8 @@ def w_decode_layer(torch, dev):
             w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8).to(dev)
             s = (torch.rand(n, generator=g) * 2e-3 + 1e-3).float().to(dev)
             pairs[id(mods[name])] = (types.SimpleNamespace(_qdata=w, _params=types.SimpleNamespace(scale=s)), None)
+        for names in (("q", "k", "v"), ("gate", "up")):
+            int8_gemv.register_siblings([(mods[n], *shapes[n], torch.int8, 256) for n in names])
         kv = [torch.randn(1, cap, Hkv, 128, generator=g).float().to(dev) for _ in range(2)]
         # each step's input is a tensor of its own, as each token's is: no rotation carries over between steps
         layers.append((mods, kv, torch.randn(1, 1, D, generator=g).float().to(dev)))

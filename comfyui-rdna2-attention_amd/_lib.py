@@ -37,6 +37,7 @@ SIGNATURES = {
     "rda_rotate": (_i, [_p, _p, _i, _i, _p]),
     "rda_gemv_i8": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _p]),
     "rda_rotate_gemv_i8": (_i, [_p, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
+    "rda_gemv_i8_multi": (_i, [_p, _i, _i, _i, _p, _p, _p, _p, _p, _i, _p, _p]),
     "rda_gemv_bf16": (_i, [_p, _p, _p, _i, _i, _p]),
     "rda_attn_decode": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _f, _p]),
     "rda_attn_merge": (_i, [_p, _p, _p, _i, _p]),

@@ -74,11 +74,12 @@ __device__ __forceinline__ int ro_of_value(int v, int steps) {  // the f4 holdin
     const int t = v - steps * 1024;
     return ro_f4(steps, (t >> 2) & 1, t >> 3);
 }
+// Bytes of LDS of x in reading order for K values.
+static inline size_t ro_lds_bytes(int K) { return (size_t)16 * RO_ROW * (4 * (K / 1024) + (K % 1024 ? 2 : 0)); }
 // Bytes of LDS the fused rotation needs for K values: the larger of the two layouts.
 static inline size_t rot_lds_bytes(int K) {
-    const int rows = 4 * (K / 1024) + (K % 1024 ? 2 : 0);
-    const size_t nat = (size_t)K + K / 4 + K / 16, ro = (size_t)4 * rows * RO_ROW;
-    return 4 * (nat > ro ? nat : ro);
+    const size_t nat = 4 * ((size_t)K + K / 4 + K / 16), ro = ro_lds_bytes(K);
+    return nat > ro ? nat : ro;
 }
 
 // The NT threads of the workgroup take x in sets of 16 consecutive values, set q = thread + NT r (r < RS). rot_load
@@ -354,6 +355,136 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_split_kernel(const void
     else ((float*)out)[row] = total;
 }
 
+// Several GEMVs over one input row in one launch: the linears that one parent forward applies to the same activation
+// (q, k and v of an attention layer; gate and up of an MLP). Matrix i takes blocks first[i] .. first[i + 1] - 1 and
+// splits its K over parts[i] waves per row -- the split gemv_i8_dispatch would choose for it alone -- so that each
+// output is the one-matrix launch's, bit for bit: parts 1 is gemv_i8_kernel's arithmetic (one row per wave, every
+// step in order, then the wave sum), parts 2 or 4 gemv_i8_split_kernel's (each wave its K / parts slice, the partial
+// sums added in part order). x is staged once per workgroup in LDS in rot_to_lds's reading order (ro_f4), rotated
+// there first when group is nonzero, and all the block's loads are issued before any arithmetic, x first.
+#define MULTI_MAX 4
+struct GemvTable {
+    const int8_t* w[MULTI_MAX];
+    const float* scale[MULTI_MAX];
+    const float* bias[MULTI_MAX];
+    void* out[MULTI_MAX];
+    int n[MULTI_MAX];
+    int parts[MULTI_MAX];
+    int first[MULTI_MAX + 1];
+    int count;
+};
+
+// The rows of matrix `mi` in block `blk` of its range, with S waves per row and GW steps of 1024 per wave at most
+// (steps past K / 1024 / S re-read an in-bounds chunk and are skipped). XS: float4s (fp16: 4-vectors) of x per
+// thread without the rotation; RS: sets of 16 values per thread with it.
+template <int GW, int S, bool TAIL, bool XH, bool ROT, int XS, int RS>
+__device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, const GemvTable& t, int mi, int blk, int K, int group,
+                                                float* __restrict__ rot_out, f4* xs, float* part_s) {
+    constexpr int RPB = GI_WAVES / S;
+    const int steps = K / 1024, wsteps = steps / S;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row = blk * RPB + wave / S, part = wave % S;
+    const int N = t.n[mi];
+    const bool active = row < N;
+    const int8_t* base = t.w[mi] + (size_t)(active ? row : 0) * K + part * wsteps * 1024;
+    typedef typename std::conditional<XH, h4v, f4>::type xv_t;
+    xv_t xr[XS];
+    f4 xq[RS][4];
+    if constexpr (ROT) {
+        rot_load<GI_WAVES * 64, RS>((const float*)xin, K, xq);
+    } else {
+#pragma unroll
+        for (int j = 0; j < XS; j++) {
+            const int i = threadIdx.x + j * GI_WAVES * 64;
+            xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
+        }
+    }
+    const float sc = t.scale[mi][active ? row : 0];
+    __builtin_amdgcn_sched_barrier(0);  // x and the scale go out before the weights
+    u4v v[GW];
+    u2v vt;
+#pragma unroll
+    for (int g = 0; g < GW; g++) {
+        v[g] = __builtin_nontemporal_load((const u4v*)(base + (g < wsteps ? g * 1024 + lane * 16 : lane * 16)));
+        __builtin_amdgcn_sched_barrier(0);  // step order, the order of the products
+    }
+    if constexpr (TAIL) vt = __builtin_nontemporal_load((const u2v*)(base + steps * 1024 + lane * 8));
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (ROT) {
+        rot_to_lds<GI_WAVES * 64, RS>(xq, xs, K, group, steps, blockIdx.x == 0 ? rot_out : nullptr);
+    } else {
+#pragma unroll
+        for (int j = 0; j < XS; j++) {
+            const int i = threadIdx.x + j * GI_WAVES * 64;
+            if (i < K / 4) {
+                f4 x;
+                if constexpr (XH) x = (f4){(float)xr[j][0], (float)xr[j][1], (float)xr[j][2], (float)xr[j][3]};
+                else x = xr[j];
+                xs[ro_of_value(4 * i, steps)] = x;
+            }
+        }
+    }
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < GW; g++) {
+        if (g >= wsteps) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f4 xv = xs[ro_f4(part * wsteps + g, j, lane)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[g][j], i), xv[i], acc);
+        }
+    }
+    if constexpr (TAIL) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const f4 xv = xs[ro_f4(steps, j, lane)];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[j], i), xv[i], acc);
+        }
+    }
+    float sum = wave_sum(acc);
+    if constexpr (S > 1) {
+        if (lane == 0) part_s[wave] = sum;
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int p2 = 1; p2 < S; p2++) sum += part_s[wave + p2];
+    }
+    if (!active || lane != 0) return;
+    sum *= sc;
+    const float* bias = t.bias[mi];
+    if (bias) sum = sum + bias[row];
+    if (XH) ((half_t*)t.out[mi])[row] = to_half(sum);
+    else ((float*)t.out[mi])[row] = sum;
+}
+
+// G: steps of 1024 values in flight for a one-row-per-wave matrix, >= K / 1024 (4 or 8: K <= 8192).
+template <int G, bool TAIL, bool XH, bool ROT>
+__global__ __launch_bounds__(GI_WAVES * 64) void gemv_multi_kernel(const void* __restrict__ xin, GemvTable t, int K, int group,
+                                                                   float* __restrict__ rot_out) {
+    constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;
+    constexpr int RS = (64 * G + (TAIL ? 32 : 0) + GI_WAVES * 64 - 1) / (GI_WAVES * 64) < 2 ? 1 : 2;
+    extern __shared__ f4 xs[];
+    __shared__ float part_s[GI_WAVES];
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < MULTI_MAX; i++)
+        if (i < t.count && (int)blockIdx.x >= t.first[i]) mi = i;
+    const int blk = blockIdx.x - t.first[mi];
+    switch (t.parts[mi]) {  // uniform over the workgroup
+    case 4:
+        if constexpr (!TAIL && G >= 4) gemv_multi_rows<G / 4, 4, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        break;
+    case 2:
+        if constexpr (!TAIL && G >= 2) gemv_multi_rows<G / 2, 2, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        break;
+    default: gemv_multi_rows<G, 1, TAIL, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+    }
+}
+
 // logits[n] = sum_k bf16(w[n, k]) x[k] (int8_gemv.hip:87-119): 8 weights per lane per step of 512, a
 // last half step of 256 when K % 512 == 256.
 __device__ __forceinline__ float bf16_dot4(u32 a, u32 b, f4 xv, float acc) {
@@ -611,26 +742,33 @@ static int launch_gemv_g(const void* x, int x_half, const void* w, const float* 
     }
 }
 
+// Waves per row of the GEMV of N rows of K values. Up to 2048 rows, split K: 4 waves per row up to 1024 rows, 2 up to
+// 2048 (K = 4096: N = 1024 3.56 -> 3.01 us; from 4096 rows on, one row per wave already gives every CU two or more
+// blocks and measured as fast or faster), where K / 1024 splits into the per-wave step counts the split kernel is
+// built for; 1 otherwise. rda_gemv_i8_multi gives each of its matrices the same split.
+static int gemv_parts(int N, int K) {
+    if (K % 1024 != 0 || N > 2048) return 1;
+    const int steps = K / 1024, S = N <= 1024 ? 4 : 2;
+    if (steps % S != 0) return 1;
+    const int g = steps / S;
+    return g == 1 || g == 2 || g == 4 || (S == 2 && g == 8) ? S : 1;
+}
+
 // The GEMV launch of rda_gemv_i8 (ROT false) and rda_rotate_gemv_i8 (ROT true, fp32 x): arguments already checked.
 template <bool ROT>
 static int gemv_i8_dispatch(const void* x, int x_half, const void* w, const float* scale, const float* bias, void* out, int N, int K, int group, float* rot_out,
                             void* stream) {
     const int steps = K / 1024;
-    // Up to 2048 rows, split K: 4 waves per row up to 1024 rows, 2 up to 2048 (K = 4096: N = 1024 3.56 -> 3.01 us;
-    // from 4096 rows on, one row per wave already gives every CU two or more blocks and measured as fast or faster).
-    if (K % 1024 == 0 && N <= 2048) {
-        const int S = N <= 1024 ? 4 : 2;
-        if (steps % S == 0) {
-            switch (S * 100 + steps / S) {
-            case 401: return launch_gemv_split<4, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 402: return launch_gemv_split<4, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 404: return launch_gemv_split<4, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 201: return launch_gemv_split<2, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 202: return launch_gemv_split<2, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 204: return launch_gemv_split<2, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            case 208: return launch_gemv_split<2, 8, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
-            default: break;
-            }
+    if (const int S = gemv_parts(N, K); S > 1) {
+        switch (S * 100 + steps / S) {
+        case 401: return launch_gemv_split<4, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 402: return launch_gemv_split<4, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 404: return launch_gemv_split<4, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 201: return launch_gemv_split<2, 1, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 202: return launch_gemv_split<2, 2, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 204: return launch_gemv_split<2, 4, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        case 208: return launch_gemv_split<2, 8, ROT>(x, x_half, w, scale, bias, out, N, K, group, rot_out, stream);
+        default: return RDA_ERR_INVALID;  // gemv_parts returns only the splits listed here
         }
     }
     // fp16 x up to 4096 rows: one row per wave with the lane's x read straight into registers (the split kernel with
@@ -672,7 +810,57 @@ int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* sc
     if (N <= 0 || K <= 0 || K % 512 != 0 || K > 16384) return RDA_ERR_INVALID;
     if (group != 4 && group != 16 && group != 64 && group != 256) return RDA_ERR_INVALID;
     if (((uintptr_t)x | (uintptr_t)rotated) & 15) return RDA_ERR_INVALID;  // read and written in 16-byte vectors
+    // The first workgroup writes `rotated` while later ones may still be reading x: the two must not overlap.
+    if (rotated && (uintptr_t)rotated < (uintptr_t)(x + K) && (uintptr_t)x < (uintptr_t)(rotated + K)) return RDA_ERR_INVALID;
     return gemv_i8_dispatch<true>(x, 0, w, scale, bias, out, N, K, group, rotated, stream);
+}
+
+int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const void* const* w, const float* const* scale, const float* const* bias,
+                      void* const* out, const int* n, int K, float* rotated, void* stream) {
+    if (count < 1 || count > MULTI_MAX || !w || !scale || !out || !n) return RDA_ERR_INVALID;
+    if (K <= 0 || K % 512 != 0 || K > 8192) return RDA_ERR_INVALID;
+    if (group != 0 && group != 4 && group != 16 && group != 64 && group != 256) return RDA_ERR_INVALID;
+    if ((group != 0 && x_half) || (group == 0 && rotated)) return RDA_ERR_INVALID;  // the rotation takes fp32 x
+    if (((uintptr_t)x | (uintptr_t)rotated) & 15) return RDA_ERR_INVALID;  // read and written in 16-byte vectors
+    const char *xb = (const char*)x, *rb = (const char*)rotated;
+    if (rotated && rb < xb + 4 * (size_t)K && xb < rb + 4 * (size_t)K) return RDA_ERR_INVALID;  // see rda_rotate_gemv_i8
+    GemvTable t = {};
+    t.count = count;
+    long blocks = 0;
+    for (int i = 0; i < count; i++) {
+        if (n[i] <= 0 || !w[i] || !scale[i] || !out[i]) return RDA_ERR_INVALID;
+        t.w[i] = (const int8_t*)w[i];
+        t.scale[i] = scale[i];
+        t.bias[i] = bias ? bias[i] : nullptr;
+        t.out[i] = out[i];
+        t.n[i] = n[i];
+        t.parts[i] = gemv_parts(n[i], K);
+        t.first[i] = (int)blocks;
+        const int rpb = GI_WAVES / t.parts[i];
+        blocks += (n[i] + rpb - 1) / rpb;
+        if (blocks > 0x7fffffff) return RDA_ERR_INVALID;
+    }
+    for (int i = count; i <= MULTI_MAX; i++) t.first[i] = (int)blocks;
+    const bool tail = K % 1024 != 0, big = K > 4096;
+    const size_t lds = group ? rot_lds_bytes(K) : ro_lds_bytes(K);
+    const dim3 grid((unsigned)blocks), block(GI_WAVES * 64);
+    hipStream_t st = (hipStream_t)stream;
+#define RDA_MULTI(G, T, XH, R) hipLaunchKernelGGL((gemv_multi_kernel<G, T, XH, R>), grid, block, lds, st, x, t, K, group, rotated)
+    if (group) {
+        if (tail) RDA_MULTI(8, true, false, true);
+        else if (big) RDA_MULTI(8, false, false, true);
+        else RDA_MULTI(4, false, false, true);
+    } else if (x_half) {
+        if (tail) RDA_MULTI(8, true, true, false);
+        else if (big) RDA_MULTI(8, false, true, false);
+        else RDA_MULTI(4, false, true, false);
+    } else {
+        if (tail) RDA_MULTI(8, true, false, false);
+        else if (big) RDA_MULTI(8, false, false, false);
+        else RDA_MULTI(4, false, false, false);
+    }
+#undef RDA_MULTI
+    return (int)hipGetLastError();
 }
 
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream) {

@@ -870,6 +870,8 @@ static int dispatch(const void* a, const void* w, const float* as, const float* 
                     int group, const void* R, const void* G, int L, void* stream) {
     if (M <= 0 || N <= 0 || K <= 0 || N % 64 != 0 || K % BK != 0) return RDA_ERR_INVALID;
     if (R && (!G || L <= 0)) return RDA_ERR_INVALID;
+    // The activations, the output and the residual operands move in 16-byte vectors (the weight may sit anywhere).
+    if (((uintptr_t)a | (uintptr_t)c | (uintptr_t)R | (uintptr_t)G) & 15) return RDA_ERR_INVALID;
     {
         const int e = dispatch8<W4, EPI>(a, w, as, ws, gs, bias, c, M, N, K, group, R, G, L, stream);
         if (e >= 0) return e;

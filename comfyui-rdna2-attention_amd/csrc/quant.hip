@@ -318,6 +318,9 @@ static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq,
 template <int ACT, bool I4, int GROUP>
 static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
     if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || (GROUP != 0 && K > MAX_LDS_K)) return RDA_ERR_INVALID;
+    // Rows are read (and the int8 rows written) in 16-byte vectors: every row must start on a 16-byte boundary.
+    if (M > 1 && (ldx < (ACT == SITU ? 2L * K : (long)K) || ldx % 8 != 0)) return RDA_ERR_INVALID;
+    if (((uintptr_t)x | (uintptr_t)u | (uintptr_t)aq | (uintptr_t)mod.w | (uintptr_t)mod.s | (uintptr_t)mod.t) & 15) return RDA_ERR_INVALID;
     if constexpr (ACT == MOD || GROUP == 0) {
         return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
     } else {

@@ -62,9 +62,17 @@ def quantized(M, row_bytes, device):
 
 
 def _rows(x):
-    """x as rows the quantization kernels can address by a row pitch: contiguous last dimension, rows not overlapping."""
-    if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) < x.shape[1]):
-        return x.contiguous()
+    """x as rows the quantization kernels can address by a row pitch: contiguous last dimension, rows not overlapping,
+    and every row starting on a 16-byte boundary (the kernels read rows in 16-byte vectors)."""
+    if x.stride(-1) != 1 or (x.shape[0] > 1 and (x.stride(0) < x.shape[1] or x.stride(0) % 8)) or x.data_ptr() % 16:
+        return x.clone(memory_format=torch.contiguous_format)
+    return x
+
+
+def _dense(x):
+    """x contiguous and 16-byte aligned (a contiguous view at an odd offset is copied)."""
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        return x.clone(memory_format=torch.contiguous_format)
     return x
 
 
@@ -76,7 +84,7 @@ def quantize(quant, x, K, up=None, group=ROT_GROUP):
     packed_a, a_scale = quantized(M, K, x.device)
     p = _lib.ptr
     if quant is k.swiglu_rot_quant_pack_a or quant is k.gate_rot_quant_pack_a:  # both operands at a pitch of K
-        x, up = x.contiguous(), up.contiguous()
+        x, up = _dense(x), _dense(up)
     else:
         x = _rows(x)
     if quant is k.quant_pack_a:
@@ -98,6 +106,8 @@ def run(quant, gemm, x, weight, weight_scale, bias, K, up=None, activations=None
     if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)
         return out
     packed_a, a_scale = quantize(quant, x, K, up, group) if activations is None else activations
+    if res is not None:  # the epilogue reads the residual and its gate in 16-byte vectors
+        res = (_dense(res[0]), _dense(res[1]))
     p = _lib.ptr
     if gemm is k.gemm_i4:
         launch(gemm, 0, 0, 0, [p(packed_a), p(weight), p(a_scale), p(weight_scale), p(bias), p(out), M, N, K])
@@ -282,9 +292,9 @@ def quantize_block_input(x, norm, scale, shift):
     global shared
     B, L, K = x.shape
     packed_a, a_scale = quantized(B * L, K, x.device)
-    x = x.contiguous()  # read at a row pitch of K
-    weight = comfy.model_management.cast_to(norm.scale, dtype=torch.float32, device=x.device)
-    s, t = (1 + scale).contiguous(), shift.contiguous()
+    x = _dense(x)  # read at a row pitch of K, in 16-byte vectors
+    weight = _dense(comfy.model_management.cast_to(norm.scale, dtype=torch.float32, device=x.device))
+    s, t = _dense(1 + scale), _dense(shift)
     p = _lib.ptr
     launch(get_kernels().mod_rot_quant_pack_a, B * L, 1, ROT_THREADS,
            [p(x), p(packed_a), p(a_scale), B * L, K, p(weight), p(s), p(t), L, float(norm.eps)])

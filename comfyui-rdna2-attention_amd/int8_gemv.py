@@ -6,7 +6,10 @@ logits, and decode attention splits the cached positions of each KV head into SP
 softmaxes are merged by a second launch. The decode launches have a fixed grid and read the cache length on the
 device, so a captured HIP graph stays valid as the cache grows.
 """
+import contextlib
+import ctypes
 import functools
+import weakref
 
 import torch
 import torch.nn.functional as F
@@ -62,17 +65,140 @@ def quantized_weight(module, weight_dtype, x):
 
 def rotate(x, group):
     """ConvRot of every `group` values of fp32 x (group a power of 4), scaled by 1 / sqrt(group)."""
+    if x.dtype != torch.float32 or x.numel() % group:
+        raise ValueError(f"rotate takes fp32 values in whole groups of {group}, not {x.numel()} of {x.dtype}")
+    x = x.contiguous()
     rotated = torch.empty_like(x)
     launch(get_kernels().rotate, x.numel() // group, 1, 256, [_lib.ptr(x), _lib.ptr(rotated), x.numel() // group, group])
     return rotated
 
 
-# The ConvRot of the last single-token input. Consecutive linears that read the same activation -- q, k and v of an
-# attention layer, gate and up of an MLP -- rotate it once. An entry is reused only for the same tensor object (held
-# here, so its memory cannot be handed to another tensor meanwhile), at the same version counter (in-place writes
-# bump it; inference tensors have none, and are matched by object alone), the same group, and the same graph-capture
-# state (a rotation launched outside a capture is never read inside one, nor the reverse).
-_last_rotation = None
+def _row(x, K, dtypes, what):
+    """x as one contiguous, 16-byte aligned row of K values of one of `dtypes` (the GEMVs read it in 16-byte vectors and
+    trust its length), or ValueError."""
+    if x.dtype not in dtypes or x.numel() != K:
+        raise ValueError(f"{what} takes {K} values of {' or '.join(str(d) for d in dtypes)}, not {x.numel()} of {x.dtype}")
+    if not x.is_contiguous() or x.data_ptr() % 16:
+        x = x.clone(memory_format=torch.contiguous_format)
+    return x
+
+
+def gemv(x, weight, scale, bias=None):
+    """out[n] = scale[n] * dot(weight[n], x) (+ bias[n]) for one row x (K values, fp32 or fp16; the output has its dtype),
+    weight (N, K) int8, scale (N,) fp32, bias (N,) fp32 or None."""
+    N, K = weight.shape
+    x = _row(x, K, (torch.float32, torch.float16), "gemv")
+    out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
+    p = _lib.ptr
+    launch(get_kernels().gemv_i8, N // BLOCK_ROWS, 1, 256, [p(x), int(x.dtype == torch.float16), p(weight), p(scale), p(bias), p(out), N, K])
+    return out
+
+
+def _rotated_buffer(rotated, K):
+    if rotated is not None and (rotated.dtype != torch.float32 or rotated.numel() != K or not rotated.is_contiguous()):
+        raise ValueError(f"rotated must be a contiguous fp32 tensor of {K} values")
+    return rotated
+
+
+def rotate_gemv(x, group, weight, scale, bias=None, rotated=None):
+    """gemv(rotate(x, group), weight, scale, bias) as one launch, bit for bit: fp32 x of K values, the ConvRot of its
+    K / group groups done by each workgroup of the GEMV in LDS; group one of FUSED_ROTATION_GROUPS. rotated (fp32,
+    K values, not overlapping x, or None) receives rotate(x, group) as well. Returns fp32 (..., N)."""
+    if group not in FUSED_ROTATION_GROUPS:
+        raise ValueError(f"rotate_gemv rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
+    N, K = weight.shape
+    x = _row(x, K, (torch.float32,), "rotate_gemv")
+    rotated = _rotated_buffer(rotated, K)
+    out = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
+    p = _lib.ptr
+    launch(get_kernels().rotate_gemv_i8, N // BLOCK_ROWS, 1, 256, [p(x), group, p(weight), p(scale), p(bias), p(out), p(rotated), N, K])
+    return out
+
+
+MULTI_MAX = 4  # matrices per gemv_multi launch
+MULTI_MAX_K = 8192
+
+
+def gemv_multi(x, layers, group=0, rotated=None):
+    """[gemv(x, w, s, b) for w, s, b in layers] (group 0), or [rotate_gemv(x, group, w, s, b) ...] (group one of
+    FUSED_ROTATION_GROUPS, fp32 x), as one launch and bit for bit the same outputs: 1-4 weights (N_i, K) int8 over
+    one row x of K <= 8192 values. rotated as in rotate_gemv."""
+    if not 1 <= len(layers) <= MULTI_MAX:
+        raise ValueError(f"gemv_multi takes 1 to {MULTI_MAX} weights, not {len(layers)}")
+    K = layers[0][0].shape[1]
+    if group and group not in FUSED_ROTATION_GROUPS:
+        raise ValueError(f"gemv_multi rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
+    x = _row(x, K, (torch.float32,) if group else (torch.float32, torch.float16), "gemv_multi")
+    rotated = _rotated_buffer(rotated, K)
+    outs, n = [], []
+    for w, s, b in layers:
+        if w.dim() != 2 or w.shape[1] != K or w.dtype != torch.int8 or not w.is_contiguous():
+            raise ValueError("gemv_multi weights are contiguous int8 (N, K) matrices of one K")
+        if s.numel() != w.shape[0] or (b is not None and b.numel() != w.shape[0]):
+            raise ValueError("gemv_multi scale and bias have one value per output")
+        outs.append(torch.empty((*x.shape[:-1], w.shape[0]), dtype=x.dtype, device=x.device))
+        n.append(w.shape[0])
+    c = len(layers)
+    ptrs = lambda ts: (ctypes.c_void_p * c)(*[None if t is None else t.data_ptr() for t in ts])  # noqa: E731
+    biases = [b for _, _, b in layers]
+    bias_table = ptrs(biases) if any(b is not None for b in biases) else None
+    _lib.call("rda_gemv_i8_multi", _lib.ptr(x), int(x.dtype == torch.float16), group, c, ptrs([w for w, _, _ in layers]),
+              ptrs([s for _, s, _ in layers]), bias_table, ptrs(outs), (ctypes.c_int * c)(*n), K, _lib.ptr(rotated))
+    return outs
+
+
+# Sibling linears: the single-token int8 linears that one parent forward applies to the same input, in a row -- q, k
+# and v of an attention layer, gate and up of an MLP (patch() registers them from the module tree). The first of them
+# to be called computes all of them with one gemv_multi launch (one ConvRot, one pass over x) and leaves the others'
+# outputs here; each is handed out once, to the call of its own module with the same input tensor object at the same
+# version (in-place writes bump it) and the same graph-capture state and stream. Any other linear_forward call, a
+# mismatch, or a repeated call clears what is left, so that outputs are never stale across calls that do not share
+# their input. Inference tensors carry no version counter: for them an in-place write to the input between two
+# siblings of one parent forward goes unseen (the parent forwards patched here never write it).
+def _ref(obj):
+    """A weak reference where the object allows one (modules do), else a strong one."""
+    try:
+        return weakref.ref(obj)
+    except TypeError:
+        return lambda: obj
+
+
+class Siblings:
+    def __init__(self, members):
+        self.refs = [_ref(m[0]) for m in members]  # modules by reference: a registration does not keep a model alive
+        self.shapes = [m[1:] for m in members]  # (N, K, weight_dtype, group)
+        self.index = {id(m[0]): i for i, m in enumerate(members)}
+
+    def modules(self):
+        return [r() for r in self.refs]
+
+
+_siblings = {}  # id(module) -> Siblings
+_stash = None  # (siblings, x, version, capture key, {member index: output})
+
+
+def register_siblings(members):
+    """Registers linears (module, N, K, weight_dtype, group) that one parent forward calls in a row on one input; they
+    must share K, the weight dtype and the ConvRot group, and K must fit one gemv_multi launch."""
+    if not 2 <= len(members) <= MULTI_MAX or len({m[2:] for m in members}) != 1 or members[0][2] > MULTI_MAX_K:
+        raise ValueError("siblings are 2-4 linears of one K (<= 8192), weight dtype and ConvRot group")
+    group = Siblings(list(members))
+    for m in members:
+        _siblings[id(m[0])] = group
+
+
+def _siblings_of(module):
+    sib = _siblings.get(id(module))
+    if sib is not None and sib.modules()[sib.index[id(module)]] is not module:  # a registered module died, its id reused
+        del _siblings[id(module)]
+        return None
+    return sib
+
+
+def forget_siblings():
+    global _stash
+    _siblings.clear()
+    _stash = None
 
 
 def _version(x):
@@ -82,82 +208,58 @@ def _version(x):
         return None
 
 
-def _capturing(x):
-    return x.is_cuda and torch.cuda.is_current_stream_capturing()
+def _capture_key(x):
+    return (torch.cuda.is_current_stream_capturing(), torch.cuda.current_stream(x.device).cuda_stream) if x.is_cuda else None
 
 
-def cached_rotation(x, group):
-    """The rotation remembered for this same input x and group, or None."""
-    hit = _last_rotation
-    if hit is not None and hit[0] is x and hit[1] == _version(x) and hit[2] == group and hit[3] == _capturing(x):
-        return hit[4]
-    return None
-
-
-def remember_rotation(x, group, rotated):
-    global _last_rotation
-    _last_rotation = (x, _version(x), group, _capturing(x), rotated)
-
-
-def rotate_once(x, group):
-    """rotate(x, group), or the rotation of the previous call when it had this same input."""
-    rotated = cached_rotation(x, group)
-    if rotated is None:
-        rotated = rotate(x, group)
-        remember_rotation(x, group, rotated)
-    return rotated
-
-
-def forget_rotation():
-    global _last_rotation
-    _last_rotation = None
-
-
-def gemv(x, weight, scale, bias=None):
-    """out[n] = scale[n] * dot(weight[n], x) (+ bias[n]) for one row x (K values, fp32 or fp16; the output has its dtype),
-    weight (N, K) int8, scale (N,) fp32, bias (N,) fp32 or None."""
-    if x.data_ptr() % 16:  # the kernels read x in 16-byte vectors
-        x = x.clone()
-    N, K = weight.shape
-    out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
-    p = _lib.ptr
-    launch(get_kernels().gemv_i8, N // BLOCK_ROWS, 1, 256, [p(x), int(x.dtype == torch.float16), p(weight), p(scale), p(bias), p(out), N, K])
+def _take_stashed(sib, module, x):
+    """The output the first sibling computed for this module and this same input, or None; clears the stash unless
+    other siblings still have outputs waiting."""
+    global _stash
+    st, _stash = _stash, None
+    if st is None or sib is None or st[0] is not sib or st[1] is not x or st[2] != _version(x) or st[3] != _capture_key(x):
+        return None
+    out = st[4].pop(sib.index[id(module)], None)
+    if out is not None and st[4]:
+        _stash = st
     return out
 
 
-def rotate_gemv(x, group, weight, scale, bias=None, rotated=None):
-    """gemv(rotate(x, group), weight, scale, bias) as one launch, bit for bit: fp32 x of K values (contiguous), the
-    ConvRot of its K / group groups done by each workgroup of the GEMV in LDS; group one of FUSED_ROTATION_GROUPS.
-    rotated (fp32, K values, or None) receives rotate(x, group) as well. Returns fp32 (..., N)."""
-    if group not in FUSED_ROTATION_GROUPS:
-        raise ValueError(f"rotate_gemv rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
-    if x.data_ptr() % 16:  # the kernel reads x in 16-byte vectors
-        x = x.clone()
-    N, K = weight.shape
-    out = torch.empty((*x.shape[:-1], N), dtype=torch.float32, device=x.device)
-    p = _lib.ptr
-    launch(get_kernels().rotate_gemv_i8, N // BLOCK_ROWS, 1, 256, [p(x), group, p(weight), p(scale), p(bias), p(out), p(rotated), N, K])
-    return out
+def _siblings_forward(sib, module, weight_dtype, group, x, x_in):
+    """Runs every sibling on x (fp32, one row) in one launch; returns this module's output and stashes the others."""
+    global _stash
+    with contextlib.ExitStack() as stack:
+        layers = []
+        for m in sib.modules():
+            weight, bias = stack.enter_context(quantized_weight(m, weight_dtype, x))
+            layers.append((weight._qdata, weight._params.scale.to(device=x.device), bias))
+        outs = gemv_multi(x, layers, group if group in FUSED_ROTATION_GROUPS else 0)
+    mine = sib.index[id(module)]
+    _stash = (sib, x_in, _version(x_in), _capture_key(x_in), {i: o for i, o in enumerate(outs) if i != mine})
+    return outs[mine]
 
 
 def linear_forward(module, N, K, weight_dtype, group, x, *args, **kwargs):
-    """Int8 Linear.forward for text generation (int8_gemv.py:48-64): one token goes to the GEMV; several tokens of a
-    generate() prefill with a large ConvRot group use a dequantized matmul; everything else keeps the layer's forward."""
+    """Int8 Linear.forward for text generation (int8_gemv.py:48-64): one token goes to the GEMV (with its registered
+    siblings, all in one launch); several tokens of a generate() prefill with a large ConvRot group use a dequantized
+    matmul; everything else keeps the layer's forward."""
     single = x.numel() == K
+    sib = _siblings_of(module)
+    stashed = _take_stashed(sib, module, x)
+    if stashed is not None:
+        return stashed
     if x.dtype != torch.float32 or patched(module) or not (single or (group > FAST_DEQUANT_GROUP and generating)):
         return type(module).forward(module, x, *args, **kwargs)
-    x = x.contiguous()
+    x_in, x = x, x.contiguous()
+    fused = single and (not group or (group in FUSED_ROTATION_GROUPS and fuse_rotation(K)))
+    if fused and sib is not None and all(m is not None and not patched(m) for m in sib.modules()):
+        return _siblings_forward(sib, module, weight_dtype, group, x, x_in)
     with quantized_weight(module, weight_dtype, x) as (weight, bias):
         scale = weight._params.scale.to(device=x.device)
+        if single and group in FUSED_ROTATION_GROUPS and fuse_rotation(K):
+            return rotate_gemv(x, group, weight._qdata, scale, bias)
         if group:
-            rotated = cached_rotation(x, group)
-            if rotated is None and single and group in FUSED_ROTATION_GROUPS and fuse_rotation(K):
-                # the first linear of this input rotates it inside its GEMV launch and keeps the rotation for the next
-                rotated = torch.empty_like(x)
-                out = rotate_gemv(x, group, weight._qdata, scale, bias, rotated)
-                remember_rotation(x, group, rotated)
-                return out
-            x = rotate_once(x, group) if rotated is None else rotated
+            x = rotate(x, group)
         if not single:
             return F.linear(x, weight._qdata.to(x.dtype) * scale, bias)
         return gemv(x, weight._qdata, scale, bias)
@@ -174,14 +276,14 @@ def mlp_forward(module, weight_dtype, x, norm=None):
 
 
 def generate(transformer, *args, **kwargs):
-    global generating
+    global generating, _stash
     generating = True
-    forget_rotation()
+    _stash = None
     try:
         return type(transformer).generate(transformer, *args, **kwargs)
     finally:
         generating = False
-        forget_rotation()
+        _stash = None
 
 
 def logits_gemv(x, weight):
@@ -237,15 +339,30 @@ def _int8_gemv_layer(module):
     return N % BLOCK_ROWS == 0 and K % STEP == 0 and params.scale.numel() == N and params.scale.dtype == torch.float32 and not params.transposed
 
 
+SIBLING_NAMES = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))  # linears a parent forward applies to one input
+
+
+def _gemv_args(module):
+    """(module, N, K, weight dtype, ConvRot group) of an int8 layer, as linear_forward takes them."""
+    N, K = module.weight.shape
+    params = module.weight._params
+    return module, N, K, module.weight.dtype, params.convrot_groupsize if params.convrot else 0
+
+
 def patch(clip):
     """Single token steps of text generation read int8 and bf16 weights directly instead of dequantizing them on every token
-    (int8_gemv.py:129-148)."""
+    (int8_gemv.py:129-148). The linears that one parent applies to the same input (SIBLING_NAMES) are registered as
+    siblings, so that a token runs them in one GEMV launch."""
     for name, module in clip.patcher.model.named_modules():
+        for names in SIBLING_NAMES:
+            layers = [getattr(module, n, None) for n in names]
+            if all(layer is not None and _int8_gemv_layer(layer) for layer in layers):
+                members = [_gemv_args(layer) for layer in layers]
+                if len({m[2:] for m in members}) == 1 and members[0][2] <= MULTI_MAX_K:
+                    register_siblings(members)
         if _int8_gemv_layer(module):
-            N, K = module.weight.shape
-            params = module.weight._params
-            group = params.convrot_groupsize if params.convrot else 0
-            clip.patcher.add_object_patch(f"{name}.forward", functools.partial(linear_forward, module, N, K, module.weight.dtype, group))
+            module, N, K, dtype, group = _gemv_args(module)
+            clip.patcher.add_object_patch(f"{name}.forward", functools.partial(linear_forward, module, N, K, dtype, group))
         elif (isinstance(module, MLP) and not module.merged_mlp and getattr(module.gate_proj, "quant_format", None) == "int8_tensorwise"
               and module.up_proj.quant_format == "int8_tensorwise"):
             clip.patcher.add_object_patch(f"{name}.forward", functools.partial(mlp_forward, module, module.gate_proj.weight.dtype))

@@ -113,9 +113,21 @@ int rda_gemv_i8(const void* x, int x_half, const void* w, const float* scale, co
 /* rotate followed by gemv_i8, int8_gemv.py:58-63 (int8_gemv.hip:31-85) -- linear_forward's single-token ConvRot
  * linear -- as one launch: out (fp32) equals, bit for bit, rda_rotate of fp32 x in K / group groups of `group` (4, 16,
  * 64 or 256) followed by rda_gemv_i8 of the rotated row. `rotated` (K floats, or NULL) receives that rotation too, for
- * further linears of the same input. K % 512 == 0, K <= 16384; x and rotated 16-byte aligned; x is not modified. */
+ * further linears of the same input. K % 512 == 0, K <= 16384; x and rotated 16-byte aligned and not overlapping
+ * (RDA_ERR_INVALID otherwise); x is not modified. */
 int rda_rotate_gemv_i8(const float* x, int group, const void* w, const float* scale, const float* bias, float* out, float* rotated, int N, int K,
                        void* stream);
+
+/* `count` (1-4) gemv_i8 launches over one input row as one launch -- the sibling linears one parent forward applies
+ * to the same activation, each a linear_forward call in the reference (int8_gemv.py:48-64; q, k, v of an attention
+ * layer, gate and up of an MLP). Matrix i: w[i] int8 [n[i], K], scale[i] fp32 [n[i]], bias[i] fp32 [n[i]] (bias
+ * itself or any bias[i] may be NULL), out[i] [n[i]] in x's type. group 0: x_half as in rda_gemv_i8, and each out[i]
+ * equals rda_gemv_i8's bit for bit; group 4, 16, 64 or 256: fp32 x is rotated first and each out[i] equals
+ * rda_rotate_gemv_i8's bit for bit, `rotated` (K floats, or NULL) receiving the rotation. The pointer and size
+ * arrays are host memory, read during the call. K % 512 == 0, K <= 8192; x and rotated 16-byte aligned and not
+ * overlapping. */
+int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const void* const* w, const float* const* scale, const float* const* bias,
+                      void* const* out, const int* n, int K, float* rotated, void* stream);
 
 /* gemv_bf16, int8_gemv.py:97 (int8_gemv.hip:87-119): fp32 logits of a bf16 table. K % 256 == 0, N % 8 == 0. */
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream);

@@ -83,6 +83,31 @@ def test_library_loads_and_binds(built):
     assert lib.rda_attn_i8_workspace(1, 24, 4096) == 24 * 4096 * 132
 
 
+def test_argument_checks_reject_before_any_launch(built):
+    """Checks that return RDA_ERR_INVALID before the device is touched (the pointers are never dereferenced): the
+    fused rotation's output overlapping its input, rows or outputs not on 16-byte boundaries, and the multi-matrix
+    GEMV's table limits."""
+    lib = _lib.declare(ctypes.CDLL(built))
+    a = 1 << 20  # a 16-byte aligned address, never read
+    K = 4096
+    for rotated in (a, a + 4 * K - 16, a - 4 * K + 16):  # the same buffer, overlapping from above and from below
+        assert lib.rda_rotate_gemv_i8(a, 256, a, a, None, a, rotated, 64, K, None) == 1
+    assert lib.rda_rot_quant_pack_a(a + 2, K, a, a, 4, K, 256, None) == 1  # row 0 misaligned
+    assert lib.rda_rot_quant_pack_a(a, K + 4, a, a, 4, K, 256, None) == 1  # pitch not a multiple of 8 values
+    assert lib.rda_rot_quant_pack_a(a, K - 8, a, a, 4, K, 256, None) == 1  # rows overlapping
+    assert lib.rda_situ_rot_quant_pack_a(a, K, a, a, 4, K, 256, None) == 1  # [hidden | gate] rows of 2K values
+    assert lib.rda_swiglu_rot_quant_pack_a(a, a + 8, a, a, 4, K, 256, None) == 1
+    assert lib.rda_gemm(a, a, a, a, None, a + 2, 256, 256, 256, None, None, 1, None) == 1  # output misaligned
+    assert lib.rda_gemm(a, a, a, a, None, a, 256, 256, 256, a + 8, a, 1, None) == 1  # residual misaligned
+    ptrs = (ctypes.c_void_p * 2)(a, a)
+    n = (ctypes.c_int * 2)(64, 64)
+    assert lib.rda_gemv_i8_multi(a, 0, 256, 0, ptrs, ptrs, None, ptrs, n, K, None, None) == 1  # no matrices
+    assert lib.rda_gemv_i8_multi(a, 0, 256, 5, ptrs, ptrs, None, ptrs, n, K, None, None) == 1  # more than 4
+    assert lib.rda_gemv_i8_multi(a, 0, 256, 2, ptrs, ptrs, None, ptrs, n, 12288, None, None) == 1  # K past 8192
+    assert lib.rda_gemv_i8_multi(a, 1, 256, 2, ptrs, ptrs, None, ptrs, n, K, None, None) == 1  # fp16 x with a rotation
+    assert lib.rda_gemv_i8_multi(a, 0, 256, 2, ptrs, ptrs, None, ptrs, n, K, a + 16, None) == 1  # rotation onto x
+
+
 def test_no_cpu_fallback_without_gpu(monkeypatch):
     """The product path raises when the GPU is missing; it never computes on the CPU."""
     import torch

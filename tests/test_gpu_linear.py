@@ -285,19 +285,30 @@ def test_w4a8_other_scale_groups_bit_exact(dev, scale_group):
     assert_same(bits(out), bits(ref))
 
 
-@pytest.mark.parametrize("layout", ["every_other_column", "transposed"])
+@pytest.mark.parametrize("layout", ["every_other_column", "transposed", "offset_columns", "odd_pitch"])
 def test_linears_take_strided_activations(dev, layout):
-    """Activations whose last dimension is not contiguous are copied into rows before the quantization pass: the
-    W4A8 and W8A8 linears give the results of the contiguous input."""
+    """Activations the quantization pass cannot read as 16-byte aligned rows -- a last dimension that is not
+    contiguous, rows starting one value into their storage (big[:, 1:K + 1]), a row pitch that is not a multiple of 8
+    values -- are copied into rows first: the W4A8 and W8A8 linears give the results of the contiguous input."""
     M, N, K = 512, 256, 1024
+    print(f"strided activations {layout}", flush=True)
     x = activations(M, K, seed=61, outliers=0)
     if layout == "every_other_column":
         big = torch.zeros(M, 2 * K, dtype=torch.float16, device=dev)
         big[:, ::2] = x.to(dev)
         xv = big[:, ::2]
-    else:
+    elif layout == "transposed":
         xv = x.t().contiguous().to(dev).t()
-    assert xv.stride(-1) != 1
+    elif layout == "offset_columns":
+        big = torch.zeros(M, K + 8, dtype=torch.float16, device=dev)
+        big[:, 1:K + 1] = x.to(dev)
+        xv = big[:, 1:K + 1]
+        assert xv.data_ptr() % 16
+    else:
+        big = torch.zeros(M, K + 4, dtype=torch.float16, device=dev)
+        big[:, :K] = x.to(dev)
+        xv = big[:, :K]
+        assert xv.stride(0) % 8
     w, wp = int4_weights(N, K, seed=62)
     gs = (torch.rand(N, K // 128, generator=gen(63)) * 1.5e-2 + 5e-3).half()
     q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())

@@ -61,41 +61,115 @@ def test_linear_forward_single_token(dev, monkeypatch, N, K, bias, group):
     assert np.all(err <= bound), f"max err {err.max():.3e}"
 
 
-def test_linear_forward_single_token_fuses_the_rotation(dev, monkeypatch):
-    """q, k and v read one input: the first single-token linear runs the ConvRot inside its GEMV launch
-    (rda_rotate_gemv_i8), which also stores the rotation; k and v reuse that stored rotation with the plain GEMV. Every
-    output equals rotate then gemv bit for bit, the stored rotation equals rotate's, and after an in-place write to
-    the input the next call rotates the new values."""
-    K = 4096
-    layers, pairs = [], {}
-    for i, N in enumerate((4096, 1024, 1024)):
-        w, s = int8_weights(N, K, seed=40 + i), channel_scales(N, seed=50 + i)
+def _weights(shapes, K, seed, bias=False, dev="cuda"):
+    out = []
+    for i, N in enumerate(shapes):
+        w, s = int8_weights(N, K, seed=seed + i), channel_scales(N, seed=seed + 10 + i)
+        b = torch.randn(N, generator=gen(seed + 20 + i)).float().to(dev) if bias and i % 2 == 0 else None
+        out.append((w.to(dev), s.to(dev), b))
+    return out
+
+
+@pytest.mark.parametrize("shapes,K,group,half", [
+    ((4096, 1024, 1024), 4096, 256, False),   # q|k|v of a Qwen3-8B layer: one row per wave + split-by-4 rows
+    ((12288, 12288), 4096, 256, False),        # gate|up
+    ((2048, 512, 64, 16), 4096, 64, False),    # split by 2 and 4, a partial last block
+    ((1024, 4096), 8192, 16, False),           # 8 steps per row: split 4 with 2 steps per wave
+    ((2560, 512, 512), 2560, 256, False),      # K with a half step (one row per wave throughout)
+    ((4096, 1024, 1024), 4096, 0, False),      # already rotated input
+    ((4096, 1024, 1024), 4096, 0, True),       # fp16 input and outputs
+    ((3072, 1000), 3584, 4, False),            # odd N, half step, group 4
+])
+def test_gemv_multi_equals_one_launch_per_matrix(dev, shapes, K, group, half):
+    """rda_gemv_i8_multi gives each matrix, bit for bit, what its own rda_gemv_i8 / rda_rotate_gemv_i8 launch gives,
+    and the same stored rotation."""
+    print(f"gemv_multi shapes={shapes} K={K} group={group} half={half}", flush=True)
+    layers = _weights(shapes, K, seed=70, bias=True, dev=dev)
+    x = torch.randn(1, K, generator=gen(71)).to(dev)
+    x = x.half() if half else x
+    kept = torch.empty(K, device=dev) if group else None
+    outs = int8_gemv.gemv_multi(x, layers, group, kept)
+    for (w, s, b), out in zip(layers, outs):
+        ref = int8_gemv.rotate_gemv(x, group, w, s, b) if group else int8_gemv.gemv(x, w, s, b)
+        assert out.dtype == ref.dtype and out.shape == ref.shape
+        assert torch.equal(out, ref), f"N={w.shape[0]}: {(out != ref).sum().item()} outputs differ"
+    if group:
+        assert torch.equal(kept.view(1, K), int8_gemv.rotate(x, group))
+        assert torch.equal(int8_gemv.gemv_multi(x, layers, group)[0], outs[0])  # without a rotation to store
+
+
+def _layers_for_linear_forward(monkeypatch, shapes, K, seed, dev):
+    mods, pairs = [], {}
+    for N, (w, s, b) in zip(shapes, _weights(shapes, K, seed, dev=dev)):
         layer = int8_layer()
-        pairs[id(layer)] = (types.SimpleNamespace(_qdata=w.to(dev), _params=types.SimpleNamespace(scale=s.to(dev))), None)
-        layers.append((layer, N, w.to(dev), s.to(dev)))
+        pairs[id(layer)] = (types.SimpleNamespace(_qdata=w, _params=types.SimpleNamespace(scale=s)), b)
+        mods.append((layer, N, w, s))
     stand_in_comfy(monkeypatch, pairs)
-    int8_gemv.forget_rotation()
-    x = torch.randn(1, 1, K, generator=gen(60)).float().to(dev)
-    rotated = int8_gemv.rotate(x, 256)
+    return mods
+
+
+def test_sibling_linears_run_as_one_launch(dev, monkeypatch):
+    """q, k and v registered as siblings: one gemv_multi launch for the three single-token linear_forward calls, each
+    output equal bit for bit to its own rotate then GEMV; after an in-place write to the input the next sibling call
+    computes from the new values."""
+    K = 4096
+    mods = _layers_for_linear_forward(monkeypatch, (4096, 1024, 1024), K, 40, dev)
+    int8_gemv.forget_siblings()
+    int8_gemv.register_siblings([(m, N, K, torch.int8, 256) for m, N, _, _ in mods])
     calls = []
-    fused = int8_gemv.rotate_gemv
-    monkeypatch.setattr(int8_gemv, "rotate_gemv", lambda *a, **k: calls.append(1) or fused(*a, **k))
-    for layer, N, w, s in layers:
-        out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
-        assert torch.equal(out, int8_gemv.gemv(rotated, w, s))
-    assert len(calls) == 1, "k and v did not reuse the stored rotation"
-    assert torch.equal(int8_gemv._last_rotation[4], rotated)
-    x.mul_(-0.5)
-    layer, N, w, s = layers[0]
-    out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
-    assert len(calls) == 2 and torch.equal(out, int8_gemv.gemv(int8_gemv.rotate(x, 256), w, s))
-    int8_gemv.forget_rotation()
+    multi = int8_gemv.gemv_multi
+    monkeypatch.setattr(int8_gemv, "gemv_multi", lambda *a, **k: calls.append(1) or multi(*a, **k))
+    try:
+        x = torch.randn(1, 1, K, generator=gen(60)).float().to(dev)
+        for _ in range(2):
+            rotated = int8_gemv.rotate(x, 256)
+            for layer, N, w, s in mods:
+                out = int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+                assert out.shape == (1, 1, N) and torch.equal(out, int8_gemv.gemv(rotated, w, s))
+            x.mul_(-0.5)
+        assert len(calls) == 2
+    finally:
+        int8_gemv.forget_siblings()
 
 
-def test_linear_forward_prefill_shares_one_rotation(dev, monkeypatch):
-    """A generate() prefill (3 tokens, ConvRot group 1024): q, k and v read one input, the first linear rotates it and
-    the next two reuse that rotation (int8_gemv's rotate_once) for their dequantized matmuls; each output matches
-    the oracle, and after an in-place write to the input the next call rotates the new values. Bound: 1e-4 of
+def test_sibling_outputs_stay_inside_their_graph(dev, monkeypatch):
+    """Two graphs captured over the same input tensor, each running q, k and v as siblings: replaying only the second,
+    after new values are written into the input, gives every sibling the second graph's own result for those values
+    (no output of the first capture is handed to the second)."""
+    K = 4096
+    mods = _layers_for_linear_forward(monkeypatch, (4096, 1024, 1024), K, 40, dev)
+    int8_gemv.forget_siblings()
+    int8_gemv.register_siblings([(m, N, K, torch.int8, 256) for m, N, _, _ in mods])
+    try:
+        x = torch.randn(1, 1, K, generator=gen(61)).float().to(dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graphs, outs = [], []
+        with torch.cuda.stream(side):
+            for layer, N, _, _ in mods:  # warm-up on the capture stream
+                int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x)
+            for _ in range(2):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=side):
+                    outs.append([int8_gemv.linear_forward(layer, N, K, torch.int8, 256, x) for layer, N, _, _ in mods])
+                graphs.append(graph)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for trial in range(3):
+            print(f"sibling graph replay {trial}", flush=True)
+            x.copy_(torch.randn(1, 1, K, generator=gen(62 + trial)).to(dev))
+            graphs[1].replay()
+            torch.cuda.synchronize()
+            rotated = int8_gemv.rotate(x, 256)
+            for (layer, N, w, s), out in zip(mods, outs[1]):
+                assert torch.equal(out, int8_gemv.gemv(rotated, w, s))
+    finally:
+        int8_gemv.forget_siblings()
+
+
+def test_linear_forward_prefill_rotates_each_call(dev, monkeypatch):
+    """A generate() prefill (3 tokens, ConvRot group 1024): q, k and v each rotate their input and run the dequantized
+    matmul; each output matches the oracle, also after an in-place write to the input. Bound: 1e-4 of
     scale * sum_k |w x| (fp32 matmul of 4096 terms)."""
     K, T, group = 4096, 3, 1024
     layers, pairs = [], {}
@@ -107,7 +181,6 @@ def test_linear_forward_prefill_shares_one_rotation(dev, monkeypatch):
         layers.append((layer, N, w, s))
     stand_in_comfy(monkeypatch, pairs)
     monkeypatch.setattr(int8_gemv, "generating", True)
-    int8_gemv.forget_rotation()
     x = torch.randn(1, T, K, generator=gen(60)).float().to(dev)
 
     def check(layer, N, w, s, out):
@@ -117,16 +190,11 @@ def test_linear_forward_prefill_shares_one_rotation(dev, monkeypatch):
         bound = 1e-4 * (np.abs(xr) @ np.abs(wd).T) * np.abs(s.numpy()) + 1e-12
         assert np.all(np.abs(out.cpu().double().numpy().reshape(T, N) - ref) <= bound)
 
-    outs = [int8_gemv.linear_forward(layer, N, K, torch.int8, group, x) for layer, N, _, _ in layers]
-    rotated = int8_gemv._last_rotation[4]
-    for (layer, N, w, s), out in zip(layers, outs):
-        check(layer, N, w, s, out)
+    for layer, N, w, s in layers:
+        check(layer, N, w, s, int8_gemv.linear_forward(layer, N, K, torch.int8, group, x))
     x.mul_(-0.5)
-    layer, N, w, s = layers[0]
-    out = int8_gemv.linear_forward(layer, N, K, torch.int8, group, x)
-    assert int8_gemv._last_rotation[4] is not rotated
-    check(layer, N, w, s, out)
-    int8_gemv.forget_rotation()
+    layer, N, w, s = layers[1]
+    check(layer, N, w, s, int8_gemv.linear_forward(layer, N, K, torch.int8, group, x))
 
 
 def test_logits_of_the_last_position(dev, monkeypatch):

@@ -84,13 +84,22 @@ def test_int8_gemv_patch_installs_eligible_objects(gemv_fakes):
         "bad_format": Linear(64, 512, fmt="float8"),
         "mlp": MLP(),
         "mlp_merged": MLP(merged=True),
+        "attn": types.SimpleNamespace(q_proj=Linear(512, 512), k_proj=Linear(128, 512), v_proj=Linear(128, 512)),
+        "attn_mixed": types.SimpleNamespace(q_proj=Linear(512, 512), k_proj=Linear(128, 512, convrot=True), v_proj=Linear(128, 512)),
         "qwen": BaseQwen3(),
         "qwen_lm_head": BaseQwen3(lm_head=True),
     }
     clip = types.SimpleNamespace(patcher=Patcher(named(types.SimpleNamespace(), tree)))
+    int8_gemv.forget_siblings()
     int8_gemv.patch(clip)
     p = clip.patcher.patches
     assert set(p) == {"ok.forward", "ok_plain.forward", "mlp.forward", "qwen.logits", "qwen.generate", "qwen.model.init_kv_cache"}
+    # siblings: q/k/v and gate/up of one parent with one K, weight dtype and ConvRot group (not the mixed-group set)
+    attn, mixed = tree["attn"], tree["attn_mixed"]
+    assert int8_gemv._siblings_of(attn.k_proj).modules() == [attn.q_proj, attn.k_proj, attn.v_proj]
+    assert int8_gemv._siblings_of(tree["mlp"].up_proj).modules() == [tree["mlp"].gate_proj, tree["mlp"].up_proj]
+    assert all(int8_gemv._siblings_of(m) is None for m in (mixed.q_proj, mixed.k_proj, tree["ok"]))
+    int8_gemv.forget_siblings()
     assert p["ok.forward"].func is int8_gemv.linear_forward and p["ok.forward"].args == (tree["ok"], 4096, 4096, torch.int8, 256)
     assert p["ok_plain.forward"].args[-1] == 0  # no ConvRot: group 0
     assert p["mlp.forward"].func is int8_gemv.mlp_forward and p["mlp.forward"].args == (tree["mlp"], torch.int8)
@@ -437,72 +446,134 @@ def test_package_without_comfyui_defines_no_nodes():
     assert pkg.io is None and not hasattr(pkg, "RDNA2Attention")
 
 
-def test_rotation_reused_by_consecutive_linears(monkeypatch):
-    """rotate_once: one rotation for consecutive linears on the same input (q/k/v, gate/up); a new one for another
-    object, another group, after an in-place write, and after generate() starts or ends."""
+def _gemv_layer(N, K):
+    m = types.SimpleNamespace(weight_function=None, bias_function=None)
+    m.qweight = types.SimpleNamespace(_qdata=torch.zeros(N, K, dtype=torch.int8), _params=types.SimpleNamespace(scale=torch.ones(N)))
+    return m
+
+
+def _record_gemv_kernels(monkeypatch, calls):
+    """Stand-ins for the GEMV launches (no GPU here): each records its call and the sum of the input it saw, and
+    returns outputs that name the call (value = number of the call) so that a stale hand-out is visible."""
+    def out(n):
+        return torch.full((n,), float(len(calls)))
+
+    def multi(x, layers, group=0, rotated=None):
+        calls.append(("multi", group, float(x.sum()), tuple(w.shape[0] for w, _, _ in layers)))
+        return [out(w.shape[0]) for w, _, _ in layers]
+
+    monkeypatch.setattr(int8_gemv, "gemv_multi", multi)
+    monkeypatch.setattr(int8_gemv, "rotate_gemv", lambda x, group, w, s, b=None, rotated=None: calls.append(("fused", group, float(x.sum()))) or out(w.shape[0]))
+    monkeypatch.setattr(int8_gemv, "rotate", lambda x, group: calls.append(("rotate", group, x.shape[-1])) or x * 2)
+    monkeypatch.setattr(int8_gemv, "gemv", lambda x, w, s, b=None: calls.append(("gemv", float(x.sum()), w.shape[1])) or out(w.shape[0]))
+
+
+def test_sibling_linears_run_in_one_launch(monkeypatch):
+    """q, k and v registered as siblings: the first call runs all three in one gemv_multi launch and k and v receive
+    its outputs; a new input object, an in-place write (version counter), an interleaved other linear, a repeated
+    call and generate() all make the next sibling compute afresh, never a stale output."""
+    cast_context(monkeypatch)
     calls = []
-    monkeypatch.setattr(int8_gemv, "rotate", lambda x, group: calls.append(group) or x * 2)
-    int8_gemv.forget_rotation()
-    x = torch.randn(1, 512)
-    a = int8_gemv.rotate_once(x, 256)
-    assert int8_gemv.rotate_once(x, 256) is a and int8_gemv.rotate_once(x, 256) is a and len(calls) == 1
-    int8_gemv.rotate_once(x, 64)
-    assert len(calls) == 2
-    b = int8_gemv.rotate_once(x, 64)
-    x.add_(1)  # an in-place write bumps the version counter
-    c = int8_gemv.rotate_once(x, 64)
-    assert c is not b and len(calls) == 3 and torch.equal(c, x * 2)
-    int8_gemv.rotate_once(x.clone(), 64)
-    assert len(calls) == 4
-    with torch.inference_mode():
-        z = torch.randn(1, 512)
-        assert int8_gemv.rotate_once(z, 256) is int8_gemv.rotate_once(z, 256) and len(calls) == 5
+    _record_gemv_kernels(monkeypatch, calls)
+    int8_gemv.forget_siblings()
+    K = 4096
+    q, k, v, o = _gemv_layer(4096, K), _gemv_layer(1024, K), _gemv_layer(1024, K), _gemv_layer(4096, K)
+    int8_gemv.register_siblings([(q, 4096, K, torch.int8, 256), (k, 1024, K, torch.int8, 256), (v, 1024, K, torch.int8, 256)])
+    lin = lambda m, x: int8_gemv.linear_forward(m, m.qweight._qdata.shape[0], K, torch.int8, 256, x)  # noqa: E731
+    x = torch.ones(1, K)
+    outs = [lin(m, x) for m in (q, k, v)]
+    assert calls == [("multi", 256, 4096.0, (4096, 1024, 1024))] and [float(t[0]) for t in outs] == [1, 1, 1]
+    lin(o, outs[0].view(1, K))  # not a sibling: its own fused rotation + GEMV
+    assert calls[-1][0] == "fused" and len(calls) == 2
+    # k first this time: any sibling may lead; a repeated call computes again
+    lin(k, x)
+    lin(k, x)
+    assert [c[0] for c in calls[2:]] == ["multi", "multi"]
+    assert float(lin(q, x)[0]) == 4 and float(lin(v, x)[0]) == 4  # the second of those launches
+    # an in-place write between siblings bumps the version counter: k computes on the new values
+    assert float(lin(q, x)[0]) == 5
+    x.mul_(-0.5)
+    assert float(lin(k, x)[0]) == 6 and calls[-1] == ("multi", 256, -2048.0, (4096, 1024, 1024))
+    assert float(lin(q, x)[0]) == 6 and len(calls) == 6
+    # another object with equal values, and a linear in between, both force a new launch
+    assert float(lin(k, x.clone())[0]) == 7
+    assert float(lin(q, x)[0]) == 8
+    lin(o, x)
+    assert float(lin(v, x)[0]) == 10
+    assert [c[0] for c in calls[6:]] == ["multi", "multi", "fused", "multi"]
 
     class T:
         def generate(self):
             return "tokens"
 
-    int8_gemv.rotate_once(x, 64)
+    lin(q, x)
     int8_gemv.generate(T())
-    int8_gemv.rotate_once(x, 64)
-    assert len(calls) == 7
+    lin(k, x)
+    assert [c[0] for c in calls[-2:]] == ["multi", "multi"]
+    int8_gemv.forget_siblings()
 
 
-def test_single_token_linears_fuse_the_first_rotation(monkeypatch):
-    """linear_forward's single-token path (int8_gemv.py:58-63): the first linear of an input rotates it inside its GEMV
-    launch and keeps the rotation; the next linears of that input (k and v after q) run the plain GEMV on it; a new
-    input fuses again, K = 12288 too; K = 9728 (past 8192 with a half step), a group outside FUSED_ROTATION_GROUPS and
-    no group take rotate then GEMV, or the plain GEMV. Kernel calls are recorded by stand-ins (no GPU here)."""
+def test_inference_mode_write_between_linears_is_seen(monkeypatch):
+    """Under torch.inference_mode() (no version counters, as ComfyUI runs nodes) an in-place write to an input between
+    two linears that are not registered siblings reaches the second: each computes from the values it is given."""
     cast_context(monkeypatch)
     calls = []
+    _record_gemv_kernels(monkeypatch, calls)
+    int8_gemv.forget_siblings()
+    K = 4096
+    a, b = _gemv_layer(64, K), _gemv_layer(64, K)
+    with torch.inference_mode():
+        x = torch.ones(1, K)
+        int8_gemv.linear_forward(a, 64, K, torch.int8, 256, x)
+        x.mul_(-0.5)
+        int8_gemv.linear_forward(b, 64, K, torch.int8, 256, x)
+        int8_gemv.linear_forward(a, 64, K, torch.int8, 0, x)
+    assert calls == [("fused", 256, 4096.0), ("fused", 256, -2048.0), ("gemv", -2048.0, K)]
 
-    def fused(x, group, w, s, b=None, rotated=None):
-        calls.append(("fused", group, w.shape[1]))
-        rotated.copy_(x * 2)
-        return torch.zeros(w.shape[0])
 
-    monkeypatch.setattr(int8_gemv, "rotate_gemv", fused)
-    monkeypatch.setattr(int8_gemv, "rotate", lambda x, group: calls.append(("rotate", group, x.shape[-1])) or x * 2)
-    monkeypatch.setattr(int8_gemv, "gemv", lambda x, w, s, b=None: calls.append(("gemv", float(x.sum()), w.shape[1])) or torch.zeros(w.shape[0]))
-
-    def layer(N, K):
-        m = types.SimpleNamespace(weight_function=None, bias_function=None)
-        m.qweight = types.SimpleNamespace(_qdata=torch.zeros(N, K, dtype=torch.int8), _params=types.SimpleNamespace(scale=torch.ones(N)))
-        return m
-
-    int8_gemv.forget_rotation()
+def test_single_token_linears_without_siblings(monkeypatch):
+    """linear_forward's single-token path (int8_gemv.py:58-63) for a linear with no registered siblings: the ConvRot
+    inside the GEMV launch for the fused groups up to K = 8192 and past it when K % 1024 == 0 (K = 12288); K = 9728
+    (past 8192 with a half step), a group outside FUSED_ROTATION_GROUPS and no group take rotate then GEMV, or the
+    plain GEMV; siblings whose K is past one gemv_multi launch are refused at registration."""
+    cast_context(monkeypatch)
+    calls = []
+    _record_gemv_kernels(monkeypatch, calls)
+    int8_gemv.forget_siblings()
     x = torch.ones(1, 4096)
-    for N in (4096, 1024, 1024):
-        int8_gemv.linear_forward(layer(N, 4096), N, 4096, torch.int8, 256, x)
-    assert calls == [("fused", 256, 4096), ("gemv", 2 * 4096.0, 4096), ("gemv", 2 * 4096.0, 4096)]
-    calls.clear()
-    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 256, torch.ones(1, 4096))  # a new input
-    assert calls == [("fused", 256, 4096)]
-    calls.clear()
-    int8_gemv.linear_forward(layer(64, 12288), 64, 12288, torch.int8, 256, torch.ones(1, 12288))  # fused
-    int8_gemv.linear_forward(layer(64, 9728), 64, 9728, torch.int8, 256, torch.ones(1, 9728))  # rotate, then GEMV
-    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 1024, x)  # group 1024: not fused
-    int8_gemv.linear_forward(layer(64, 4096), 64, 4096, torch.int8, 0, x)  # no ConvRot
-    assert calls == [("fused", 256, 12288), ("rotate", 256, 9728), ("gemv", 2 * 9728.0, 9728), ("rotate", 1024, 4096),
-                     ("gemv", 2 * 4096.0, 4096), ("gemv", 4096.0, 4096)]
-    int8_gemv.forget_rotation()
+    int8_gemv.linear_forward(_gemv_layer(64, 4096), 64, 4096, torch.int8, 256, x)
+    int8_gemv.linear_forward(_gemv_layer(64, 12288), 64, 12288, torch.int8, 256, torch.ones(1, 12288))
+    int8_gemv.linear_forward(_gemv_layer(64, 9728), 64, 9728, torch.int8, 256, torch.ones(1, 9728))
+    int8_gemv.linear_forward(_gemv_layer(64, 4096), 64, 4096, torch.int8, 1024, x)
+    int8_gemv.linear_forward(_gemv_layer(64, 4096), 64, 4096, torch.int8, 0, x)
+    assert calls == [("fused", 256, 4096.0), ("fused", 256, 12288.0), ("rotate", 256, 9728), ("gemv", 2 * 9728.0, 9728),
+                     ("rotate", 1024, 4096), ("gemv", 2 * 4096.0, 4096), ("gemv", 4096.0, 4096)]
+    with pytest.raises(ValueError):
+        int8_gemv.register_siblings([(_gemv_layer(64, 12288), 64, 12288, torch.int8, 256), (_gemv_layer(64, 12288), 64, 12288, torch.int8, 256)])
+    with pytest.raises(ValueError):
+        int8_gemv.register_siblings([(_gemv_layer(64, 4096), 64, 4096, torch.int8, 256), (_gemv_layer(64, 4096), 64, 4096, torch.int8, 64)])
+
+
+def test_gemv_wrappers_check_their_inputs():
+    """The public GEMV wrappers refuse inputs the kernels would read past (wrong dtype or length) before any launch."""
+    w, s = torch.zeros(64, 512, dtype=torch.int8), torch.ones(64)
+    with pytest.raises(ValueError):
+        int8_gemv.rotate_gemv(torch.zeros(512, dtype=torch.float16), 256, w, s)
+    with pytest.raises(ValueError):
+        int8_gemv.rotate_gemv(torch.zeros(256), 256, w, s)
+    with pytest.raises(ValueError):
+        int8_gemv.rotate_gemv(torch.zeros(512), 256, w, s, rotated=torch.zeros(512, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        int8_gemv.rotate_gemv(torch.zeros(512), 256, w, s, rotated=torch.zeros(256))
+    with pytest.raises(ValueError):
+        int8_gemv.gemv(torch.zeros(500), w, s)
+    with pytest.raises(ValueError):
+        int8_gemv.gemv(torch.zeros(512, dtype=torch.float64), w, s)
+    with pytest.raises(ValueError):
+        int8_gemv.gemv_multi(torch.zeros(512, dtype=torch.float16), [(w, s, None)], group=256)
+    with pytest.raises(ValueError):
+        int8_gemv.gemv_multi(torch.zeros(512), [(w, s, None)] * 5)
+    with pytest.raises(ValueError):
+        int8_gemv.gemv_multi(torch.zeros(512), [(w, s, None), (torch.zeros(64, 1024, dtype=torch.int8), s, None)])
+    with pytest.raises(ValueError):
+        int8_gemv.rotate(torch.zeros(500), 256)
