@@ -374,19 +374,27 @@ struct GemvTable {
     int count;
 };
 
-// The rows of matrix `mi` in block `blk` of its range, with S waves per row and GW steps of 1024 per wave at most
-// (steps past K / 1024 / S re-read an in-bounds chunk and are skipped). XS: float4s (fp16: 4-vectors) of x per
-// thread without the rotation; RS: sets of 16 values per thread with it.
-template <int GW, int S, bool TAIL, bool XH, bool ROT, int XS, int RS>
+// The rows of matrix `mi` in block `blk` of its range, with S waves per row (S = 1: RW rows per wave, rows
+// r GI_WAVES + wave of the block's RW GI_WAVES) and GW steps of 1024 per wave at most (steps past K / 1024 / S re-read
+// an in-bounds chunk and are skipped). XS: float4s (fp16: 4-vectors) of x per thread without the rotation; RS: sets
+// of 16 values per thread with it.
+template <int GW, int S, int RW, bool TAIL, bool XH, bool ROT, int XS, int RS>
 __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, const GemvTable& t, int mi, int blk, int K, int group,
                                                 float* __restrict__ rot_out, f4* xs, float* part_s) {
-    constexpr int RPB = GI_WAVES / S;
+    static_assert(S == 1 || RW == 1, "split rows take one row per wave group");
+    constexpr int RPB = GI_WAVES / S * RW;
     const int steps = K / 1024, wsteps = steps / S;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blk * RPB + wave / S, part = wave % S;
+    const int row0 = blk * RPB + wave / S, part = wave % S;
     const int N = t.n[mi];
-    const bool active = row < N;
-    const int8_t* base = t.w[mi] + (size_t)(active ? row : 0) * K + part * wsteps * 1024;
+    bool active[RW];
+    const int8_t* base[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int row = row0 + r * GI_WAVES;
+        active[r] = row < N;
+        base[r] = t.w[mi] + (size_t)(active[r] ? row : 0) * K + part * wsteps * 1024;
+    }
     typedef typename std::conditional<XH, h4v, f4>::type xv_t;
     xv_t xr[XS];
     f4 xq[RS][4];
@@ -399,16 +407,21 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
             xr[j] = ((const xv_t*)xin)[i < K / 4 ? i : 0];
         }
     }
-    const float sc = t.scale[mi][active ? row : 0];
-    __builtin_amdgcn_sched_barrier(0);  // x and the scale go out before the weights
-    u4v v[GW];
-    u2v vt;
+    float sc[RW];
 #pragma unroll
-    for (int g = 0; g < GW; g++) {
-        v[g] = __builtin_nontemporal_load((const u4v*)(base + (g < wsteps ? g * 1024 + lane * 16 : lane * 16)));
-        __builtin_amdgcn_sched_barrier(0);  // step order, the order of the products
+    for (int r = 0; r < RW; r++) sc[r] = t.scale[mi][active[r] ? row0 + r * GI_WAVES : 0];
+    __builtin_amdgcn_sched_barrier(0);  // x and the scales go out before the weights
+    u4v v[RW][GW];
+    u2v vt[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+#pragma unroll
+        for (int g = 0; g < GW; g++) {
+            v[r][g] = __builtin_nontemporal_load((const u4v*)(base[r] + (g < wsteps ? g * 1024 + lane * 16 : lane * 16)));
+            __builtin_amdgcn_sched_barrier(0);  // row and step order, the order of the products
+        }
+        if constexpr (TAIL) vt[r] = __builtin_nontemporal_load((const u2v*)(base[r] + steps * 1024 + lane * 8));
     }
-    if constexpr (TAIL) vt = __builtin_nontemporal_load((const u2v*)(base + steps * 1024 + lane * 8));
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (ROT) {
@@ -426,43 +439,49 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
         }
     }
     __syncthreads();
-    float acc = 0.f;
 #pragma unroll
-    for (int g = 0; g < GW; g++) {
-        if (g >= wsteps) continue;
+    for (int r = 0; r < RW; r++) {
+        float acc = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const f4 xv = xs[ro_f4(part * wsteps + g, j, lane)];
+        for (int g = 0; g < GW; g++) {
+            if (g >= wsteps) continue;
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[g][j], i), xv[i], acc);
+            for (int j = 0; j < 4; j++) {
+                const f4 xv = xs[ro_f4(part * wsteps + g, j, lane)];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[r][g][j], i), xv[i], acc);
+            }
+        }
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const f4 xv = xs[ro_f4(steps, j, lane)];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[r][j], i), xv[i], acc);
+            }
+        }
+        float sum = wave_sum(acc);
+        if constexpr (S > 1) {
+            if (lane == 0) part_s[wave] = sum;
+            __syncthreads();
+            if (part != 0) return;
+#pragma unroll
+            for (int p2 = 1; p2 < S; p2++) sum += part_s[wave + p2];
+        }
+        const int row = row0 + r * GI_WAVES;
+        if (active[r] && lane == 0) {
+            sum *= sc[r];
+            const float* bias = t.bias[mi];
+            if (bias) sum = sum + bias[row];
+            if (XH) ((half_t*)t.out[mi])[row] = to_half(sum);
+            else ((float*)t.out[mi])[row] = sum;
         }
     }
-    if constexpr (TAIL) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const f4 xv = xs[ro_f4(steps, j, lane)];
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[j], i), xv[i], acc);
-        }
-    }
-    float sum = wave_sum(acc);
-    if constexpr (S > 1) {
-        if (lane == 0) part_s[wave] = sum;
-        __syncthreads();
-        if (part != 0) return;
-#pragma unroll
-        for (int p2 = 1; p2 < S; p2++) sum += part_s[wave + p2];
-    }
-    if (!active || lane != 0) return;
-    sum *= sc;
-    const float* bias = t.bias[mi];
-    if (bias) sum = sum + bias[row];
-    if (XH) ((half_t*)t.out[mi])[row] = to_half(sum);
-    else ((float*)t.out[mi])[row] = sum;
 }
 
-// G: steps of 1024 values in flight for a one-row-per-wave matrix, >= K / 1024 (4 or 8: K <= 8192).
-template <int G, bool TAIL, bool XH, bool ROT>
+// G: steps of 1024 values in flight for a one-row-per-wave matrix, >= K / 1024 (4 or 8: K <= 8192). RW: rows per
+// wave of the matrices that take one wave per row.
+template <int G, int RW, bool TAIL, bool XH, bool ROT>
 __global__ __launch_bounds__(GI_WAVES * 64) void gemv_multi_kernel(const void* __restrict__ xin, GemvTable t, int K, int group,
                                                                    float* __restrict__ rot_out) {
     constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;
@@ -476,12 +495,12 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_multi_kernel(const void* _
     const int blk = blockIdx.x - t.first[mi];
     switch (t.parts[mi]) {  // uniform over the workgroup
     case 4:
-        if constexpr (!TAIL && G >= 4) gemv_multi_rows<G / 4, 4, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        if constexpr (!TAIL && G >= 4) gemv_multi_rows<G / 4, 4, 1, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
         break;
     case 2:
-        if constexpr (!TAIL && G >= 2) gemv_multi_rows<G / 2, 2, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        if constexpr (!TAIL && G >= 2) gemv_multi_rows<G / 2, 2, 1, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
         break;
-    default: gemv_multi_rows<G, 1, TAIL, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+    default: gemv_multi_rows<G, 1, RW, TAIL, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
     }
 }
 
@@ -824,6 +843,13 @@ int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const voi
     if (((uintptr_t)x | (uintptr_t)rotated) & 15) return RDA_ERR_INVALID;  // read and written in 16-byte vectors
     const char *xb = (const char*)x, *rb = (const char*)rotated;
     if (rotated && rb < xb + 4 * (size_t)K && xb < rb + 4 * (size_t)K) return RDA_ERR_INVALID;  // see rda_rotate_gemv_i8
+    // Rows per wave of the one-row-per-wave matrices: 4 or 2 where that still leaves >= 768 of their blocks (a block
+    // stages and rotates x once for all its rows: gate|up 2 x 12288 rows, K = 4096: 22.4 us at 1, 21.4 at 2, 20.3 at 4),
+    // else 1 (q|k|v: 10.7 us at 1, 12.0 at 2; o: 6.5 at 1 or 2, 8.2 at 4).
+    long rows1 = 0;
+    for (int i = 0; i < count; i++)
+        if (gemv_parts(n[i], K) == 1) rows1 += n[i] > 0 ? n[i] : 0;
+    const int rw = rows1 >= 768L * GI_WAVES * 4 ? 4 : rows1 >= 768L * GI_WAVES * 2 ? 2 : 1;
     GemvTable t = {};
     t.count = count;
     long blocks = 0;
@@ -836,7 +862,7 @@ int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const voi
         t.n[i] = n[i];
         t.parts[i] = gemv_parts(n[i], K);
         t.first[i] = (int)blocks;
-        const int rpb = GI_WAVES / t.parts[i];
+        const int rpb = t.parts[i] > 1 ? GI_WAVES / t.parts[i] : GI_WAVES * rw;
         blocks += (n[i] + rpb - 1) / rpb;
         if (blocks > 0x7fffffff) return RDA_ERR_INVALID;
     }
@@ -845,7 +871,12 @@ int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const voi
     const size_t lds = group ? rot_lds_bytes(K) : ro_lds_bytes(K);
     const dim3 grid((unsigned)blocks), block(GI_WAVES * 64);
     hipStream_t st = (hipStream_t)stream;
-#define RDA_MULTI(G, T, XH, R) hipLaunchKernelGGL((gemv_multi_kernel<G, T, XH, R>), grid, block, lds, st, x, t, K, group, rotated)
+#define RDA_MULTI(G, T, XH, R)                                                                                                \
+    do {                                                                                                                      \
+        if (rw == 1) hipLaunchKernelGGL((gemv_multi_kernel<G, 1, T, XH, R>), grid, block, lds, st, x, t, K, group, rotated);  \
+        else if (rw == 2) hipLaunchKernelGGL((gemv_multi_kernel<G, 2, T, XH, R>), grid, block, lds, st, x, t, K, group, rotated); \
+        else hipLaunchKernelGGL((gemv_multi_kernel<G, 4, T, XH, R>), grid, block, lds, st, x, t, K, group, rotated);          \
+    } while (0)
     if (group) {
         if (tail) RDA_MULTI(8, true, false, true);
         else if (big) RDA_MULTI(8, false, false, true);

@@ -79,6 +79,9 @@ def _weights(shapes, K, seed, bias=False, dev="cuda"):
     ((4096, 1024, 1024), 4096, 0, False),      # already rotated input
     ((4096, 1024, 1024), 4096, 0, True),       # fp16 input and outputs
     ((3072, 1000), 3584, 4, False),            # odd N, half step, group 4
+    ((12288, 1024, 2048), 4096, 256, False),   # two rows per wave beside split rows
+    ((12288, 12296), 2560, 256, False),        # four rows per wave, half step, a partial last block
+    ((16384, 8192), 4096, 0, True),            # four rows per wave, fp16
 ])
 def test_gemv_multi_equals_one_launch_per_matrix(dev, shapes, K, group, half):
     """rda_gemv_i8_multi gives each matrix, bit for bit, what its own rda_gemv_i8 / rda_rotate_gemv_i8 launch gives,
