@@ -9,29 +9,6 @@
 #define SPLITS 32  // position chunks per (batch, kv head) in attn_decode
 #define HEAD 128
 
-// rotate (int8_gemv.hip:31-52): H4 steps at strides 1, 4, 16, ... < group in fp32, times 1/sqrt(group).
-__global__ __launch_bounds__(256) void rotate_kernel(const float* __restrict__ x, float* __restrict__ out, int group) {
-    extern __shared__ float s[];
-    const float* in = x + (size_t)blockIdx.x * group;
-    for (int i = threadIdx.x; i < group; i += 256) s[i] = in[i];
-    __syncthreads();
-    for (int stride = 1; stride < group; stride *= 4) {
-        for (int q = threadIdx.x; q < group / 4; q += 256) {
-            const int i = (q / stride) * stride * 4 + q % stride;
-            const float a = s[i], b = s[i + stride], c = s[i + stride * 2], d = s[i + stride * 3];
-            const float sum = a + b + c + d;
-            s[i] = sum - 2.0f * d;
-            s[i + stride] = sum - 2.0f * c;
-            s[i + stride * 2] = sum - 2.0f * b;
-            s[i + stride * 3] = sum - 2.0f * a;
-        }
-        __syncthreads();
-    }
-    const float norm = 1.0f / sqrtf((float)group);
-    float* o = out + (size_t)blockIdx.x * group;
-    for (int i = threadIdx.x; i < group; i += 256) o[i] = s[i] * norm;
-}
-
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 
 // Position in the GEMVs' LDS copy of x of its f4 number i (values 4i .. 4i + 3), in reading order: the f4 j of lane
@@ -41,8 +18,8 @@ __device__ __forceinline__ int gemv_pos(int i, int steps) {
     return tail < 0 ? ((i >> 8) * 4 + (i & 3)) * 64 + ((i & 255) >> 2) : steps * 256 + (tail & 1) * 64 + (tail >> 1);
 }
 
-// One H4 step of rotate_kernel on the four values i, i + s, i + 2s, i + 3s (elementwise for f4): the same sum order,
-// so the same roundings.
+// One H4 step of the rotation on the four values i, i + s, i + 2s, i + 3s (elementwise for f4), in the sum order of
+// int8_gemv.hip:41-46, so with its roundings.
 template <typename T>
 __device__ __forceinline__ void h4_step(T& a, T& b, T& c, T& d) {
     const T sum = a + b + c + d;
@@ -59,7 +36,50 @@ __device__ __forceinline__ f4 h4_step1(f4 x) {
     return (f4){sum - 2.0f * x[3], sum - 2.0f * x[2], sum - 2.0f * x[1], sum - 2.0f * x[0]};
 }
 
-// The fused ConvRot of the GEMVs' fp32 x (rotate_kernel's arithmetic, bit for bit) goes through two LDS layouts of
+// rotate (int8_gemv.hip:31-52): every group of G = 4^n fp32 values goes through one H4 step per base-4 digit of the
+// value index, lowest digit first (strides 1, 4, 16, ... < G; each step with h4_step's sum order), then the factor
+// 1 / sqrt(G), exact. A workgroup takes one group. The group is copied into LDS (coalesced), then rotated in passes
+// of one base-16 digit: in pass k a thread takes sets of the 16 values that differ only in digit k -- set q holds
+// hi 16^(k+1) + j 16^k + lo for j < 16, lo = q mod 16^k, hi = q / 16^k -- and runs both of the digit's H4 steps in
+// registers (strides 16^k and 4 16^k: j's low and high base-4 digits); a last base-4 digit alone takes sets of 4.
+// Then the group is copied out, scaled. LDS word of value p: p + p / 16, so that the sets of a wave's lanes fall in
+// distinct banks in every pass. ceil(n / 2) + 1 barriers per group, against n + 1 for one step per barrier.
+__host__ __device__ __forceinline__ int rot_word(int p) { return p + (p >> 4); }
+
+__global__ __launch_bounds__(256) void rotate_group_kernel(const float* __restrict__ x, float* __restrict__ out, int group) {
+    extern __shared__ float gs[];
+    const float* in = x + (size_t)blockIdx.x * group;
+    for (int p = threadIdx.x; p < group; p += 256) gs[rot_word(p)] = in[p];
+    __syncthreads();
+    const int digits = __builtin_ctz(group) / 2;  // n
+    for (int k = 0, span = 1; 2 * k < digits; k++, span *= 16) {
+        const int W = 2 * k + 1 < digits ? 16 : 4;  // values per set: two base-4 digits, or the last one alone
+        for (int q = threadIdx.x; q < group / W; q += 256) {
+            const int lo = q % span, hi = q / span, first = hi * W * span + lo;
+            float v[16];
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++)
+                if (jj < W) v[jj] = gs[rot_word(first + jj * span)];
+            if (W == 16) {
+#pragma unroll
+                for (int b = 0; b < 16; b += 4) h4_step(v[b], v[b + 1], v[b + 2], v[b + 3]);  // stride 16^k
+#pragma unroll
+                for (int m = 0; m < 4; m++) h4_step(v[m], v[m + 4], v[m + 8], v[m + 12]);  // stride 4 16^k
+            } else {
+                h4_step(v[0], v[1], v[2], v[3]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 16; jj++)
+                if (jj < W) gs[rot_word(first + jj * span)] = v[jj];
+        }
+        __syncthreads();
+    }
+    const float norm = 1.0f / sqrtf((float)group);
+    float* o = out + (size_t)blockIdx.x * group;
+    for (int p = threadIdx.x; p < group; p += 256) o[p] = gs[rot_word(p)] * norm;
+}
+
+// The fused ConvRot of the GEMVs' fp32 x (rotate_group_kernel's arithmetic, bit for bit) goes through two LDS layouts of
 // one buffer (word = 4 bytes):
 // * natural: value v at word nat_word(v) = v + 4 (v >> 4) + 16 (v >> 8) -- a thread's four f4s of 16 consecutive values
 //   and the transposed words 256 b + 16 i + p (p = lane & 15, b = 4 consecutive blocks a wave) both fall in distinct
@@ -89,7 +109,7 @@ static inline size_t rot_lds_bytes(int K) {
 // 1 / sqrt(group) in reading order once every thread has read: three LDS passes, three barriers with the caller's
 // (groups of 4 and 16 write their sets in reading order straight away). With rot_out (nonzero in one workgroup) the
 // rotated values are also stored there, in natural order. group is 4, 16, 64 or 256: larger groups
-// would need LDS steps of their own (rotate_kernel then gemv_i8_kernel serve them). The caller waits at a barrier
+// would need LDS steps of their own (rotate_group_kernel then gemv_i8_kernel serve them). The caller waits at a barrier
 // before reading xs.
 template <int NT, int RS>
 __device__ __forceinline__ void rot_load(const float* __restrict__ x, int K, f4 (&v)[RS][4]) {
@@ -191,7 +211,7 @@ __device__ __forceinline__ void rot_to_lds(f4 (&v)[RS][4], f4* xs, int K, int gr
 // chunk of the row and are skipped by the products, indices of x past K / 4 re-read x[0 .. 4).
 // x sits in LDS in reading order, so that the 64 lanes of a b128 read touch consecutive addresses: the
 // f4 j of lane l in step s at (4s + j) * 64 + l, and in the half step at 256 steps + 64 j + l.
-// ROT: x (fp32) is first rotated in groups of `group` by the workgroup (rot_to_lds), bit for bit as rotate_kernel
+// ROT: x (fp32) is first rotated in groups of `group` by the workgroup (rot_to_lds), bit for bit as rotate_group_kernel
 // would, so that one launch replaces rotate + GEMV; its loads go out before the weights' as well; in ROT mode
 // the LDS copy is in rot_to_lds's padded reading order (ro_f4).
 template <int G, bool TAIL, bool XH, bool ROT, int NW>
@@ -810,7 +830,10 @@ extern "C" {
 
 int rda_rotate(const float* x, float* out, int rows, int group, void* stream) {
     if (rows <= 0 || group < 4 || group > 16384 || (group & (group - 1)) != 0 || (__builtin_ctz(group) & 1)) return RDA_ERR_INVALID;
-    hipLaunchKernelGGL(rotate_kernel, dim3(rows), dim3(256), (size_t)group * 4, (hipStream_t)stream, x, out, group);
+    const size_t lds = (size_t)rot_word(group) * 4;  // 16384 values: 68 KiB
+    static std::atomic<size_t> done[RDA_MAX_DEVICES];
+    if (const int e = ensure_dynamic_lds((const void*)rotate_group_kernel, lds, done)) return e;
+    hipLaunchKernelGGL(rotate_group_kernel, dim3(rows), dim3(256), lds, (hipStream_t)stream, x, out, group);
     return (int)hipGetLastError();
 }
 

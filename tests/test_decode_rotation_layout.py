@@ -13,6 +13,10 @@ padded reading order (f4 j of lane l in step s at (4 s + j) 77 + l + 4 (l >> 4))
 - the buffer read back in reading order equals the oracle's rotation bit for bit.
 Planted mistakes (the transposed base off by one block, the stride-4 step skipped, the half step's lane order
 dropped, an even row length) fail it.
+
+It also models rotate_group_kernel (rda_rotate, any group of 4^n up to 16384): the group in padded LDS (word
+p + p / 16), one pass per base-16 digit of the value index with each thread's sets of 16 (or 4) values in registers;
+each pass's sets partition the group, the words stay in the host's LDS size, and the result is the oracle's rotation.
 """
 import numpy as np
 import pytest
@@ -204,3 +208,95 @@ def test_model_catches_mistakes(mistake, K, group):
         xw = rot_to_lds(x, K, group, mistake=mistake)
         ref = oracle.rotate_f32(x.reshape(-1, group), group).reshape(-1)
         assert np.array_equal(read_back(xw, K, 76 if mistake == "row" else RO_ROW).view(np.uint32), ref.view(np.uint32))
+
+
+# ------------------------------------------------------------------ rotate_group_kernel (rda_rotate), any group of 4^n
+
+def rot_word(p):
+    return p + (p >> 4)
+
+
+def h4_step(a, b, c, d):
+    """The kernel's h4_step on float32 values: sum = ((a + b) + c) + d, then sum - 2 d, sum - 2 c, sum - 2 b, sum - 2 a."""
+    f = np.float32
+    s = f(f(f(a + b) + c) + d)
+    return f(s - f(2) * d), f(s - f(2) * c), f(s - f(2) * b), f(s - f(2) * a)
+
+
+def rotate_group_model(x, group, threads=256):
+    """rotate_group_kernel for one group, thread by thread and pass by pass: returns (output, LDS words touched per
+    pass as lists of (thread, word, is_write))."""
+    words = rot_word(group - 1) + 1
+    lds = np.full(words, np.nan, np.float32)
+    for p in range(group):
+        lds[rot_word(p)] = x[p]
+    digits = (group.bit_length() - 1) // 2
+    passes, k, span = [], 0, 1
+    while 2 * k < digits:
+        W = 16 if 2 * k + 1 < digits else 4
+        touched, new = [], lds.copy()
+        for t in range(threads):
+            for q in range(t, group // W, threads):
+                lo, hi = q % span, q // span
+                first = hi * W * span + lo
+                idx = [rot_word(first + j * span) for j in range(W)]
+                v = [lds[i] for i in idx]
+                if W == 16:
+                    for b in range(0, 16, 4):
+                        v[b:b + 4] = h4_step(*v[b:b + 4])
+                    for m in range(4):
+                        v[m], v[m + 4], v[m + 8], v[m + 12] = h4_step(v[m], v[m + 4], v[m + 8], v[m + 12])
+                else:
+                    v = list(h4_step(*v))
+                for i, val in zip(idx, v):
+                    new[i] = val
+                touched += [(t, i) for i in idx]
+        passes.append(touched)
+        lds = new
+        k, span = k + 1, span * 16
+    norm = np.float32(1) / np.sqrt(np.float32(group))
+    out = np.array([np.float32(lds[rot_word(p)] * norm) for p in range(group)], np.float32)
+    return out, passes, words
+
+
+@pytest.mark.parametrize("group", [4, 16, 64, 256, 1024, 4096, 16384])
+def test_rotate_group_kernel_model(group):
+    """Each pass's sets partition the group (every value read and written once, by one thread), every word lies in the
+    host's LDS size (rot_word(group) words), a wave's first-value reads of a pass fall in distinct banks (up to 2-way
+    in the stride-256 pass), and the result equals the oracle's rotation bit for bit."""
+    rng = np.random.default_rng(group)
+    x = (rng.standard_normal(group) * 3).astype(np.float32)
+    out, passes, words = rotate_group_model(x, group)
+    assert words <= rot_word(group)
+    assert len(passes) == ((group.bit_length() - 1) // 2 + 1) // 2
+    for touched in passes:
+        ws = [w for _, w in touched]
+        assert len(ws) == group and len(set(ws)) == group and max(ws) < words
+        first_reads = {}
+        for t, w in touched:
+            first_reads.setdefault(t, w)  # a thread's first word of the pass: lanes of a wave read it together
+        for wave in range(0, 256, 64):
+            banks = [first_reads[t] % 64 for t in range(wave, wave + 64) if t in first_reads]
+            if banks:
+                assert max(np.bincount(banks)) <= 2
+    ref = oracle.rotate_f32(x.reshape(1, group), group).reshape(-1)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_rotate_group_model_sees_a_skipped_step():
+    """The model is not vacuous: dropping the stride-4 step of the first pass changes the result."""
+    x = np.random.default_rng(1).standard_normal(256).astype(np.float32)
+    global h4_step
+    saved = h4_step
+    calls = []
+
+    def skip_second(a, b, c, d):
+        calls.append(1)
+        return (a, b, c, d) if len(calls) == 5 else saved(a, b, c, d)
+
+    h4_step = skip_second
+    try:
+        out, _, _ = rotate_group_model(x, 256)
+    finally:
+        h4_step = saved
+    assert not np.array_equal(out, oracle.rotate_f32(x.reshape(1, 256), 256).reshape(-1))
