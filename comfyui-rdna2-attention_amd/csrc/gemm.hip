@@ -819,18 +819,23 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
     // A and W reach LDS by 16-byte global->LDS copies (rows stay aligned: K % 64 == 0).
     if (!aligned(a, 16) || !aligned(w, 16) || !aligned(c, 16) || !aligned(ws, 16) || !aligned(bias, 8) || !aligned(R, 8) || !aligned(G, 8)) return -1;
     if constexpr (EPI == GROUP_SCALED) {
-        // One group per 128-wide slice. 128 x 128 blocks leave room for two blocks per CU, so one block's group
-        // folds (vector ALU) overlap the other's products. Each wave takes all 128 rows and 32 columns: one int4
-        // fragment to widen per k step instead of two (as 64 x 64), for two more A fragment reads from LDS.
-        // The block's group scales are staged whole (BN x K / 128 halves), so past K = 3456 two blocks no longer fit a
-        // CU's LDS: then one block per CU, which holds the scales of K up to ~45000.
+        // One group per 128-wide slice. 128 x 128 blocks of four waves leave room for two blocks per CU, so one
+        // block's group folds (vector ALU) overlap the other's products. Each wave takes all 128 rows and 32 columns:
+        // one int4 fragment to widen per k step instead of two (as 64 x 64), for two more A fragment reads from LDS.
+        // The block's group scales are staged whole (BN x K / 128 halves), so past K = 3456 two blocks no longer fit
+        // a CU's LDS: there, with N % 256 == 0, one 128 x 256 block of eight waves per CU (each A panel serving 256
+        // columns), else one 128 x 128 block, which holds the scales of K up to ~45000. In one process:
+        // 4096 x 12288 x 3072 197.0 / 198.6 us two 128 x 128 blocks per CU, 200.9 / 202.3 one 128 x 256, 217.6 one
+        // 128 x 128; 4096 x 3072 x 12288 210.8 one 128 x 256 (four stages 213.4 at two; one 128 x 128 234-239).
         if (group != 128 || K % 128 != 0 || N % 128 != 0 || !aligned(gs, 16)) return -1;
-        if (N % 256 == 0) {  // three stages (four, where they fit, measured 1.4% slower at K = 3072)
+        {
+            const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            if (e >= 0) return e;
+        }
+        if (N % 256 == 0) {
             const int e = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
             if (e >= 0) return e;
         }
-        const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
-        if (e >= 0) return e;
         return launch_gemm8<128, 128, 128, 3, W4, EPI, 1, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
     } else {
         // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
