@@ -101,7 +101,12 @@ template <bool I8, int NWV>
 __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))) void attn_kernel(AttnArgs p) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     using T = Tile<I8>;
-    constexpr int SS = (NWV == 12 ? 2 : 1) * T::BYTES;  // bytes per stage
+    // LDS: the K tiles of the three stages, then their V tiles (stage s, set c: K at s KS + c K_BYTES, V at
+    // VOFF + s VS + c V_BYTES), so that a stage's offset from the K or V base register fits the 16-bit offset field
+    // of an LDS read in every stage (with K and V stages interleaved, the third began at 64 KiB and each of its reads
+    // took a v_add).
+    constexpr int NSET = NWV == 12 ? 2 : 1;
+    constexpr int KS = NSET * T::K_BYTES, VS = NSET * T::V_BYTES, VOFF = 3 * KS;
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, lq = lane & 31;
     const int wq = __builtin_amdgcn_readfirstlane(t >> 6);  // scalar
 
@@ -216,26 +221,27 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     const u32 k_off = (u32)(row0 * skl2) + ((u32)kc << 4);
     const u32 v_off = (u32)(row0 * svl2) + ((u32)vc << 4);
     const u32 k8_off = (u32)((8 * cw + (lane >> 3)) * 128) + ((u32)((lane & 7) ^ (lane >> 3)) << 4);
-    auto issue = [&](int key0, const char* st) {
+    auto issue = [&](int key0, int stage) {
         if (!copier) return;
-        st += cset * T::BYTES;
+        const char* kst = smem + stage * KS + cset * T::K_BYTES;
+        const char* vst = smem + VOFF + stage * VS + cset * T::V_BYTES;
         if (I8) {
-            if (cw < 4) dma16((const char*)k8base + (size_t)key0 * 128, k8_off, st + cw * 1024);
-            if (cw == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, st + KB * 128);
+            if (cw < 4) dma16((const char*)k8base + (size_t)key0 * 128, k8_off, kst + cw * 1024);
+            if (cw == 0) dma4(ksbase + key0, (u32)min(lane, KB - 1) * 4, kst + KB * 128);
         }
         const char* kt = (const char*)kbase + key0 * skl2;
         const char* vt = (const char*)vbase + key0 * svl2;
         if (key0 + KB <= p.Lk) {
             if (single) {
-                if (!I8) dma16(kt, k_off, st + cw * 1024);
-                dma16(vt, v_off, st + T::K_BYTES + cw * 1024);
+                if (!I8) dma16(kt, k_off, kst + cw * 1024);
+                dma16(vt, v_off, vst + cw * 1024);
             } else {
                 if (!I8) {
 #pragma unroll
-                    for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, st + (4 * i + cw) * 1024);
+                    for (int i = 0; i < 2; i++) dma16(kt + i * 16 * skl2, k_off, kst + (4 * i + cw) * 1024);
                 }
 #pragma unroll
-                for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, st + T::K_BYTES + (4 * i + cw) * 1024);
+                for (int i = 0; i < 2; i++) dma16(vt + i * 16 * svl2, v_off, vst + (4 * i + cw) * 1024);
             }
         } else {
             // The tile's base stays in SGPRs; the lane's row (clamped to Lk - 1) enters through its 32-bit offset. The
@@ -250,8 +256,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
                 if (single && i > 0) break;
                 const int ri = single ? r0 : 16 * i + r0, di = single ? cw : 4 * i + cw;
                 const u32 r = (u32)(min(key0 + ri, p.Lk - 1) - key0);
-                if (!I8) dma16(kt, r * (u32)skl2 + kcl, st + di * 1024);
-                dma16(vt, r * (u32)svl2 + vcl, st + T::K_BYTES + di * 1024);
+                if (!I8) dma16(kt, r * (u32)skl2 + kcl, kst + di * 1024);
+                dma16(vt, r * (u32)svl2 + vcl, vst + di * 1024);
             }
         }
     };
@@ -263,17 +269,17 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     u32 ks_rd = 0;
     if (I8) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) k_rd[ks] = (u32)(set * T::BYTES + lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
-        ks_rd = (u32)(set * T::BYTES + KB * 128 + 16 * g);
+        for (int ks = 0; ks < 4; ks++) k_rd[ks] = (u32)(set * T::K_BYTES + lq * 128 + (((2 * ks + g) ^ (lq & 7)) << 4));
+        ks_rd = (u32)(set * T::K_BYTES + KB * 128 + 16 * g);
         asm volatile("" : "+v"(ks_rd));
     }
     const u32 smem_u = lds_addr(smem);  // the dynamic LDS base (0: no static LDS), folded into the per-lane offsets below
     // V^T reads: chunk 4 dt + c' of the lane's rows sits at 4 dt ^ vx, so its offset is v_base ^ 64 dt (v_base has
-    // zeros in bits 4-7 besides vx << 4, and the stage's K part is a whole number of 256-byte rows).
+    // zeros in bits 4-7 besides vx << 4: the V region and its tiles start on 256-byte boundaries).
     u32 v_base;
     {
         const int sg = lane & 15;
-        const u32 vt = smem_u + (u32)(set * T::BYTES + T::K_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
+        const u32 vt = smem_u + (u32)(VOFF + set * T::V_BYTES + (4 * g + (sg >> 2)) * 256 + (sg & 1) * 8);
         const int vx = (2 * ((lane >> 4) & 1) + ((sg & 3) >> 1)) ^ ((sg >> 2) << 2);
         v_base = vt + (u32)(vx << 4);
     }
@@ -285,7 +291,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     // The fp16 K reads of a lane: row lq of the stage, chunk 2 ks + g at (2 ks + g) ^ (lq & 15) = 2 ks ^ kx, i.e. byte
     // offset 256 lq + ((kx << 4) ^ 32 ks). The dynamic LDS starts at offset 0 (this kernel has no static LDS), so the
     // low eight bits of k_base are kx << 4 and the read for ks is k_base ^ 32 ks: one xor per read from one value.
-    u32 k_base = smem_u + (u32)(set * T::BYTES + lq * 256) + (u32)(((lane & 15) ^ g) << 4);
+    u32 k_base = smem_u + (u32)(set * T::K_BYTES + lq * 256) + (u32)(((lane & 15) ^ g) << 4);
     asm volatile("" : "+v"(k_base));
 
     // S^T of the tile in stage `stage` (a compile-time stage folds into the reads' offset fields; a runtime one is
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     // per-row factor (Q's scale times scale log2 e) enters the exponent's FMA (exps) and the slow path's maximum. The
     // steady steps run the scaling of the next tile's scores beside the PV products, where the vector ALU is idle.
     auto qk_raw = [&](auto stage, i16v& acc, auto&& hook) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * SS);
+        const u32 st_u = (u32)((int)stage * KS);
         i4v ka[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) ka[ks] = *(const i4v*)(smem + st_u + k_rd[ks]);
@@ -310,13 +316,13 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
         }
     };
     auto scale_part = [&](auto stage, const i16v& acc, float (&out)[16], int r4) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * SS);
+        const u32 st_u = (u32)((int)stage * KS);
         const f4 sc = *(const f4*)(smem + st_u + ks_rd + 32 * r4);  // the scales of keys 8 r4 + 4 g .. + 3
 #pragma unroll
         for (int e = 0; e < 4; e++) out[r4 * 4 + e] = (float)acc[r4 * 4 + e] * sc[e];  // hip_attention.hip:227
     };
     auto qk = [&](auto stage, float (&out)[16], auto&& hook) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * SS);
+        const u32 st_u = (u32)((int)stage * KS);
         if constexpr (!I8) {
             // K operands of the first 64 dims go out before the products; each operand of the second 64 is read into
             // the registers the matching first-half product has just consumed. The base passes through an empty asm
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     // O^T += V^T P^T with the V tile of stage `stage` and P in pf. Each V^T operand of the second 16-key step is read
     // into the registers the matching first-step product has just consumed.
     auto pv = [&](auto stage, auto&& hook) __attribute__((always_inline)) {
-        const u32 st_u = (u32)((int)stage * SS);
+        const u32 st_u = (u32)((int)stage * VS);
         u32 vb = v_base;
         asm volatile("" : "+v"(vb));
         auto read_v = [&](int j, int dt) __attribute__((always_inline)) {
@@ -458,7 +464,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     auto step = [&](int i, auto stage, auto kind) __attribute__((always_inline)) {
         constexpr int K = decltype(kind)::value;
         const auto next = next_stage(stage);
-        if constexpr (K == 0) issue((i + 2) * KB, smem + (int)next_stage(next) * SS);
+        if constexpr (K == 0) issue((i + 2) * KB, (int)next_stage(next));
         const float l_old = l;
         if constexpr (K != 2) {
             float nxt[16];
@@ -488,8 +494,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
         }
     };
     const int first = ((1 - tiles) % 3 + 3) % 3;  // the stage of tile 0
-    issue(0, smem + first * SS);
-    if (tiles > 1) issue(KB, smem + next_stage(first) * SS);
+    issue(0, first);
+    if (tiles > 1) issue(KB, next_stage(first));
     wait_copies();
     __syncthreads();
     if (tiles == 1) {
