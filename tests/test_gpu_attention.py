@@ -5,6 +5,8 @@ on the CPU), so it is held to a stated tolerance against the float64 closed form
 with ATOL = RTOL = 2e-3 (P is rounded to fp16 before PV, 2^-11 relative; the output to fp16). The int8-QK variant is
 checked against the closed form of its own quantized scores (the Q/K codes and int32 scores are exact) to the
 same tolerance, and its quantized K against the oracle bit for bit."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -136,6 +138,41 @@ def test_pack_k_i8_bit_exact(dev, B, Hkv, Lk):
         assert_same(k8[bh, :Lk], q_ref)
         assert_same(ks[bh, :Lk], s_ref)
         assert not k8[bh, Lk:].any()
+
+
+def test_attention_full_size_every_row(dev):
+    """The fused-attention configuration at full size (B=1, H=24, S=4096, D=128): every one of the 98,304 query rows
+    against a float64 reference computed on the GPU head by head (torch float64 matmuls and softmax), fp16 and
+    int8-QK (the latter against the softmax of its own exact quantized scores: codes from the oracle's quantizer, the
+    int32 scores exact in float64, scaled in fp32 in the kernel's order). Tolerance as everywhere in this file."""
+    B, H, L = 1, 24, 4096
+    q, k, v = qkv(B, H, H, L, L, seed=4)
+    scale = 128 ** -0.5
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    scale_log2 = np.float32(scale * math.log2(math.e))
+    for int8_qk in (False, True):
+        print(f"attention full size, every row, int8_qk={int8_qk}", flush=True)
+        out = torch.empty(B, H, L, 128, dtype=torch.float16, device=dev)
+        hip_attention.attention(qd, kd, vd, out, scale, int8_qk)
+        worst = 0.0
+        for h in range(H):
+            vh = vd[0, h].double()
+            if int8_qk:
+                q8, qs = oracle.quant_rows_rint(q[0, h].numpy())
+                k8, ks = oracle.quant_rows_rint(k[0, h].numpy())
+                si = torch.from_numpy(q8).to(dev).double() @ torch.from_numpy(k8).to(dev).double().T  # exact integers
+                sc = torch.from_numpy((qs * scale_log2).astype(np.float32)).to(dev)
+                s2 = ((si.float() * sc[:, None]) * torch.from_numpy(ks).to(dev)[None, :]).double()
+                p = torch.exp2(s2 - s2.max(dim=1, keepdim=True).values)
+            else:
+                sc = (qd[0, h].double() @ kd[0, h].double().T) * scale
+                p = torch.exp(sc - sc.max(dim=1, keepdim=True).values)
+            ref = (p @ vh) / p.sum(dim=1, keepdim=True)
+            err = (out[0, h].double() - ref).abs()
+            excess = (err - (ATOL + RTOL * ref.abs())).max().item()
+            worst = max(worst, err.max().item())
+            assert excess <= 0, f"head {h}: max abs err {err.max().item():.3e}, worst excess {excess:.3e}"
+        print(f"  max abs err over all rows {worst:.3e}", flush=True)
 
 
 def test_attention_full_size_sampled(dev):

@@ -224,6 +224,32 @@ def test_w4a8_full_size_sampled_rows(dev):
     assert_same(bits(out[rows]), bits(ref))
 
 
+def test_w4a8_full_size_every_output(dev):
+    """The W4A8 configuration at full size (4096 x 12288 x 3072): all 50 M outputs bit for bit. The reference is built
+    on the GPU from pinned pieces: the int32 partial of every 128-wide group from rda_gemm_acc on that K slice (the
+    accumulator entry point, bit-exact above), then the W4A8 epilogue evaluated in float64, where each step is exact
+    before its single rounding to fp32 -- p_g gs_g + y (p_g < 2^18, gs fp16, y fp32: the exact sum fits 53 bits, which
+    the test asserts) rounded once is the fp32 fma; y as rounded once is the fp32 product -- then fp16."""
+    M, N, K = 4096, 12288, 3072
+    x = activations(M, K, seed=7, outliers=0)
+    w, wp = int4_weights(N, K, seed=8)
+    gs = (torch.rand(N, K // 128, generator=gen(9)) * 1.5e-2 + 5e-3).half()
+    xd, wpd, gsd = x.to(dev), wp.to(dev), gs.to(dev)
+    out = int8_gemm.linear_w4a8(xd, wpd, gsd)
+    packed, a_scale = int8_gemm.quantize(kern().rot_quant_pack_a, xd, K)
+    a8 = packed.view(torch.int8)[:M * K].view(M, K)
+    y = torch.zeros(M, N, dtype=torch.float64, device=dev)
+    for g in range(K // 128):
+        print(f"w4a8 full size: group {g}", flush=True)
+        part = int8_gemm.gemm_acc(a8[:, g * 128:(g + 1) * 128].contiguous(), wpd[:, g * 64:(g + 1) * 64].contiguous(), M, 128, int4=True)
+        prod = part.double() * gsd[:, g].double()[None, :]
+        total = prod + y
+        assert torch.equal(total - y, prod), "a float64 step was inexact"
+        y = total.float().double()
+    ref = (y * a_scale.double()[:, None]).float().half()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"{(out != ref).sum().item()} outputs differ"
+
+
 def test_w4a4_hook_path_bit_exact(dev):
     """rot_quant_pack_a_i4 + gemm_i4 (the convrot_w4a4_forward replacement) against the oracle."""
     M, N, K = 600, 256, 1024
