@@ -83,9 +83,21 @@ def _row(x, K, dtypes, what):
     return x
 
 
+def _weight_args(weight, scale, bias, what):
+    """Raises ValueError unless weight is a contiguous int8 (N, K) matrix and scale (and bias, if given) contiguous fp32
+    with N values: the kernels read N fp32 scales and biases and whole weight rows."""
+    if weight.dim() != 2 or weight.dtype != torch.int8 or not weight.is_contiguous():
+        raise ValueError(f"{what} takes a contiguous int8 (N, K) weight")
+    N = weight.shape[0]
+    for name, t in (("scale", scale), ("bias", bias)):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != N or not t.is_contiguous()):
+            raise ValueError(f"{what}: {name} must be contiguous fp32 with {N} values")
+
+
 def gemv(x, weight, scale, bias=None):
     """out[n] = scale[n] * dot(weight[n], x) (+ bias[n]) for one row x (K values, fp32 or fp16; the output has its dtype),
     weight (N, K) int8, scale (N,) fp32, bias (N,) fp32 or None."""
+    _weight_args(weight, scale, bias, "gemv")
     N, K = weight.shape
     x = _row(x, K, (torch.float32, torch.float16), "gemv")
     out = torch.empty((*x.shape[:-1], N), dtype=x.dtype, device=x.device)
@@ -106,6 +118,7 @@ def rotate_gemv(x, group, weight, scale, bias=None, rotated=None):
     K values, not overlapping x, or None) receives rotate(x, group) as well. Returns fp32 (..., N)."""
     if group not in FUSED_ROTATION_GROUPS:
         raise ValueError(f"rotate_gemv rotates groups of {FUSED_ROTATION_GROUPS}, not {group}")
+    _weight_args(weight, scale, bias, "rotate_gemv")
     N, K = weight.shape
     x = _row(x, K, (torch.float32,), "rotate_gemv")
     rotated = _rotated_buffer(rotated, K)
@@ -132,10 +145,9 @@ def gemv_multi(x, layers, group=0, rotated=None):
     rotated = _rotated_buffer(rotated, K)
     outs, n = [], []
     for w, s, b in layers:
-        if w.dim() != 2 or w.shape[1] != K or w.dtype != torch.int8 or not w.is_contiguous():
-            raise ValueError("gemv_multi weights are contiguous int8 (N, K) matrices of one K")
-        if s.numel() != w.shape[0] or (b is not None and b.numel() != w.shape[0]):
-            raise ValueError("gemv_multi scale and bias have one value per output")
+        _weight_args(w, s, b, "gemv_multi")
+        if w.shape[1] != K:
+            raise ValueError("gemv_multi weights share one K")
         outs.append(torch.empty((*x.shape[:-1], w.shape[0]), dtype=x.dtype, device=x.device))
         n.append(w.shape[0])
     c = len(layers)

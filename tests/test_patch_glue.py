@@ -577,3 +577,12 @@ def test_gemv_wrappers_check_their_inputs():
         int8_gemv.gemv_multi(torch.zeros(512), [(w, s, None), (torch.zeros(64, 1024, dtype=torch.int8), s, None)])
     with pytest.raises(ValueError):
         int8_gemv.rotate(torch.zeros(500), 256)
+    for bad_scale, bad_bias in ((s.half(), None), (torch.ones(32), None), (s, torch.zeros(64, dtype=torch.float16)), (s, torch.zeros(63))):
+        with pytest.raises(ValueError):
+            int8_gemv.gemv(torch.zeros(512), w, bad_scale, bad_bias)
+        with pytest.raises(ValueError):
+            int8_gemv.rotate_gemv(torch.zeros(512), 256, w, bad_scale, bad_bias)
+        with pytest.raises(ValueError):
+            int8_gemv.gemv_multi(torch.zeros(512), [(w, bad_scale, bad_bias)])
+    with pytest.raises(ValueError):
+        int8_gemv.gemv(torch.zeros(512), w.t().contiguous().t(), s)  # a transposed (non-contiguous) weight
