@@ -211,9 +211,9 @@ def w_w4a8_gemm(torch, dev):
     k, p = int8_gemm.get_kernels(), _lib.ptr
     w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 8), dtype=torch.uint8).to(dev)
     gs = (torch.rand(N, K // 128, generator=gen(torch, 9)) * 1.5e-2 + 5e-3).half().to(dev)
-    a, s = int8_gemm.quantize(k.rot_quant_pack_a, x, K)
+    a, s = int8_gemm.quantize(k.rot_quant_pack_a_il, x, K)  # k-interleaved, as linear_w4a8 quantizes for this GEMM
     c = torch.empty(M, N, dtype=torch.float16, device=dev)
-    fn = lambda i: _lib.check(k.gemm_w4a8(p(a), p(w4), p(s), p(gs), None, p(c), M, N, K, 128, _lib.stream()))  # noqa: E731
+    fn = lambda i: _lib.check(k.gemm_w4a8_il(p(a), p(w4), p(s), p(gs), None, p(c), M, N, K, 128, _lib.stream()))  # noqa: E731
     return fn, 1, 2.0 * M * N * K, "mfma_i8", event_timed
 
 
@@ -226,9 +226,9 @@ def w_w4a8_gemm_k12288(torch, dev):
     x = torch.randn(M, K, generator=gen(torch, 23)).half().to(dev)
     w4 = torch.randint(0, 256, (N, K // 2), generator=gen(torch, 24), dtype=torch.uint8).to(dev)
     gs = (torch.rand(N, K // 128, generator=gen(torch, 25)) * 1.5e-2 + 5e-3).half().to(dev)
-    a, s = int8_gemm.quantize(k.rot_quant_pack_a, x, K)
+    a, s = int8_gemm.quantize(k.rot_quant_pack_a_il, x, K)  # k-interleaved, as linear_w4a8 quantizes for this GEMM
     c = torch.empty(M, N, dtype=torch.float16, device=dev)
-    fn = lambda i: _lib.check(k.gemm_w4a8(p(a), p(w4), p(s), p(gs), None, p(c), M, N, K, 128, _lib.stream()))  # noqa: E731
+    fn = lambda i: _lib.check(k.gemm_w4a8_il(p(a), p(w4), p(s), p(gs), None, p(c), M, N, K, 128, _lib.stream()))  # noqa: E731
     return fn, 1, 2.0 * M * N * K, "mfma_i8", event_timed
 
 

@@ -29,6 +29,8 @@ SIGNATURES = {
     "rda_gemm": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _i, _p]),
     "rda_gemm_i4": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p]),
     "rda_gemm_w4a8": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
+    "rda_rot_quant_pack_a_il": (_i, [_p, _l, _p, _p, _i, _i, _i, _p]),
+    "rda_gemm_w4a8_il": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p]),
     "rda_gemm_acc": (_i, [_p, _p, _i, _p, _i, _i, _i, _p]),
     "rda_attn": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _f, _p]),
     "rda_attn_i8_workspace": (_sz, [_i, _i, _i]),

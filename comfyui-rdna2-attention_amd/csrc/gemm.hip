@@ -410,7 +410,7 @@ __device__ __forceinline__ void epilogue_block(const i16v (&acc)[FI][FJ], const 
 // copy and fragment read is issued in the shadow of a product, spread evenly over its 32-wide k step
 // (sched_barrier pins the order). Fragments of the next k step are read during the current one; the
 // slice's barrier sits before its last k step, so the next slice's first reads start right after it.
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM, int NW>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB, int WGM, int NW, bool IL>
 __global__ __launch_bounds__(64 * NW, MINB) void gemm8_kernel(const int8_t* __restrict__ A, const int8_t* __restrict__ W, const float* __restrict__ as,
                                                       const float* __restrict__ ws, const half_t* __restrict__ gs, const half_t* __restrict__ bias,
                                                       void* __restrict__ Cout, int M, int N, int K, const half_t* __restrict__ R,
@@ -527,13 +527,20 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm8_kernel(const int8_t* __re
     auto wraw = [&](const char* st, int kk, int j) -> u2v {
         return *(const u2v*)(st + BM * KB8 + (wn * TN + j * 32 + lq) * WB + ((kk ^ fxb) << 4) + 8 * g);
     };
+    // IL: the activations are stored k-interleaved (each 8 values of k as the even ones, then the odd ones), so the
+    // even-k and odd-k bytes are the fragment's words as they are, with no interleave.
     auto widen = [](u2v p) -> i4v {
         u4v o;
 #pragma unroll
         for (int d = 0; d < 2; d++) {
             const u32 lo = (p[d] << 4) & 0xf0f0f0f0u, hi = p[d] & 0xf0f0f0f0u;  // 16 x (signed nibble) per byte
-            o[2 * d] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-            o[2 * d + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+            if constexpr (IL) {
+                o[2 * d] = lo;
+                o[2 * d + 1] = hi;
+            } else {
+                o[2 * d] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                o[2 * d + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+            }
         }
         return as_i4(o);
     };
@@ -775,7 +782,7 @@ __global__ __launch_bounds__(64 * NW, MINB) void gemm8_kernel(const int8_t* __re
     }
 }
 
-template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1, int WGM = 2, int NW = 4>
+template <int BM, int BN, int KB8, int NS, bool W4, int EPI, int MINB = 1, int WGM = 2, int NW = 4, bool IL = false>
 static int launch_gemm8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                         const void* R, const void* G, int L, void* stream) {
     const size_t stage = (size_t)BM * KB8 + (size_t)BN * (W4 ? KB8 / 2 : KB8);
@@ -783,7 +790,7 @@ static int launch_gemm8(const void* a, const void* w, const float* as, const flo
     size_t lds = EPI == RAW_ACC || stages > tile ? stages : tile;  // dynamic part; the scale block is static
     if (EPI == GROUP_SCALED) lds = (lds + 15) / 16 * 16 + (size_t)BN * (K / KB8) * 2;
     if (lds > 160 * 1024 / MINB - (size_t)(BN * 4 + SC_BIAS(BN) + BM * 4)) return -1;
-    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB, WGM, NW>;
+    auto kern = gemm8_kernel<BM, BN, KB8, NS, W4, EPI, MINB, WGM, NW, IL>;
     static std::atomic<size_t> configured[RDA_MAX_DEVICES];
     if (const int e = ensure_dynamic_lds((const void*)kern, lds, configured)) return e;
     hipLaunchKernelGGL(kern, dim3(N / BN, (M + BM - 1) / BM), dim3(64 * NW), lds, (hipStream_t)stream, (const int8_t*)a, (const int8_t*)w, as, ws,
@@ -809,7 +816,7 @@ static int gemm8_width(int M, int N) {
 }
 
 // The direct-copy kernel for this call, or -1 when the call does not fit it (the caller then uses gemm_kernel).
-template <bool W4, int EPI>
+template <bool W4, int EPI, bool IL = false>
 static int dispatch8(const void* a, const void* w, const float* as, const float* ws, const void* gs, const void* bias, void* c, int M, int N, int K,
                      int group, const void* R, const void* G, int L, void* stream) {
     if (K >= (1 << 24)) return -1;  // per-lane copy offsets (< 64 K) must fit the 32-bit voffset
@@ -829,14 +836,14 @@ static int dispatch8(const void* a, const void* w, const float* as, const float*
         // 128 x 128; 4096 x 3072 x 12288 210.8 one 128 x 256 (four stages 213.4 at two; one 128 x 128 234-239).
         if (group != 128 || K % 128 != 0 || N % 128 != 0 || !aligned(gs, 16)) return -1;
         {
-            const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            const int e = launch_gemm8<128, 128, 128, 3, W4, EPI, 2, 1, 4, IL>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
             if (e >= 0) return e;
         }
         if (N % 256 == 0) {
-            const int e = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+            const int e = launch_gemm8<128, 256, 128, 3, W4, EPI, 1, 1, 8, IL>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
             if (e >= 0) return e;
         }
-        return launch_gemm8<128, 128, 128, 3, W4, EPI, 1, 1>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
+        return launch_gemm8<128, 128, 128, 3, W4, EPI, 1, 1, 4, IL>(a, w, as, ws, gs, bias, c, M, N, K, R, G, L, stream);
     } else {
         // 128-value k slices when K allows (two stages, three for 128-wide tiles), else 64 in four stages.
         const bool wide = K % 128 == 0;
@@ -909,6 +916,15 @@ int rda_gemm_w4a8(const void* a_q, const void* w_packed, const float* a_scale, c
                   int group, void* stream) {
     if (K % 128 != 0) return RDA_ERR_INVALID;
     return dispatch<true, GROUP_SCALED>(a_q, w_packed, a_scale, nullptr, group_scales, bias, c, M, N, K, group, nullptr, nullptr, 1, stream);
+}
+
+int rda_gemm_w4a8_il(const void* a_q, const void* w_packed, const float* a_scale, const void* group_scales, const void* bias, void* c, int M, int N,
+                     int K, int group, void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128 != 0) return RDA_ERR_INVALID;
+    if (((uintptr_t)a_q | (uintptr_t)c) & 15) return RDA_ERR_INVALID;
+    // Only the direct-copy kernel reads k-interleaved activations: shapes it does not take are refused.
+    const int e = dispatch8<true, GROUP_SCALED, true>(a_q, w_packed, a_scale, nullptr, group_scales, bias, c, M, N, K, group, nullptr, nullptr, 1, stream);
+    return e >= 0 ? e : RDA_ERR_INVALID;
 }
 
 int rda_gemm_acc(const void* a_q, const void* w, int w_int4, void* acc, int M, int N, int K, void* stream) {

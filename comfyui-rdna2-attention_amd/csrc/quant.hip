@@ -112,7 +112,7 @@ __device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
 // is vector-ALU bound); MOD keeps 4 (QT threads), whose sum of squares follows the reference's thread order.
 template <int ACT, bool I4, int GROUP, int NW>
 __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
-                                                       int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod) {
+                                                       int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod, int interleave) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ float red[8];
     half_t* rotated = (half_t*)smem;
@@ -301,43 +301,51 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
             else q[i] = cvt_floor(fminf(fmaxf(d + 0.5f, -128.f), 127.f));
         }
         u4v o;
+        if (interleave) {  // k-interleaved: each 8 values of k as its 4 even ones, then its 4 odd ones
 #pragma unroll
-        for (int d = 0; d < 4; d++) o[d] = pack4(q[d * 4], q[d * 4 + 1], q[d * 4 + 2], q[d * 4 + 3]);
+            for (int d = 0; d < 4; d++) {
+                const int b = (d >> 1) * 8 + (d & 1);
+                o[d] = pack4(q[b], q[b + 2], q[b + 4], q[b + 6]);
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < 4; d++) o[d] = pack4(q[d * 4], q[d * 4 + 1], q[d * 4 + 2], q[d * 4 + 3]);
+        }
         *(u4v*)(out + ch * 16) = o;
     }
 }
 
 template <int ACT, bool I4, int GROUP, int NW>
-static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
+static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream, int il) {
     const size_t lds = GROUP ? (size_t)K * 2 + NW * 64 * 17 * sizeof(float) : K <= MAX_LDS_K ? (size_t)K * 2 : 0;
     hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
-                       (const half_t*)u, (int8_t*)aq, as, K, mod);
+                       (const half_t*)u, (int8_t*)aq, as, K, mod, il);
     return (int)hipGetLastError();
 }
 
 template <int ACT, bool I4, int GROUP>
-static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
+static int launch_rot_quant(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream, int il = 0) {
     if (M <= 0 || K <= 0 || K % (GROUP ? GROUP : 16) != 0 || (GROUP != 0 && K > MAX_LDS_K)) return RDA_ERR_INVALID;
     // Rows are read (and the int8 rows written) in 16-byte vectors: every row must start on a 16-byte boundary.
     if (M > 1 && (ldx < (ACT == SITU ? 2L * K : (long)K) || ldx % 8 != 0)) return RDA_ERR_INVALID;
     if (((uintptr_t)x | (uintptr_t)u | (uintptr_t)aq | (uintptr_t)mod.w | (uintptr_t)mod.s | (uintptr_t)mod.t) & 15) return RDA_ERR_INVALID;
     if constexpr (ACT == MOD || GROUP == 0) {
-        return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
+        return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream, il);
     } else {
         // One wave per 1024 values, up to four: every lane has a chunk in both passes when K is a multiple of 1024.
         switch (K >= 4096 ? 4 : K <= 1024 ? 1 : K / 1024) {
-        case 1: return launch_rot_quant_nw<ACT, I4, GROUP, 1>(x, ldx, u, aq, as, M, K, mod, stream);
-        case 2: return launch_rot_quant_nw<ACT, I4, GROUP, 2>(x, ldx, u, aq, as, M, K, mod, stream);
-        case 3: return launch_rot_quant_nw<ACT, I4, GROUP, 3>(x, ldx, u, aq, as, M, K, mod, stream);
-        default: return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream);
+        case 1: return launch_rot_quant_nw<ACT, I4, GROUP, 1>(x, ldx, u, aq, as, M, K, mod, stream, il);
+        case 2: return launch_rot_quant_nw<ACT, I4, GROUP, 2>(x, ldx, u, aq, as, M, K, mod, stream, il);
+        case 3: return launch_rot_quant_nw<ACT, I4, GROUP, 3>(x, ldx, u, aq, as, M, K, mod, stream, il);
+        default: return launch_rot_quant_nw<ACT, I4, GROUP, 4>(x, ldx, u, aq, as, M, K, mod, stream, il);
         }
     }
 }
 
 template <int ACT, bool I4>
-static int dispatch_group(int group, const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream) {
-    if (group == 256) return launch_rot_quant<ACT, I4, 256>(x, ldx, u, aq, as, M, K, mod, stream);
-    if (group == 128) return launch_rot_quant<ACT, I4, 128>(x, ldx, u, aq, as, M, K, mod, stream);
+static int dispatch_group(int group, const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream, int il = 0) {
+    if (group == 256) return launch_rot_quant<ACT, I4, 256>(x, ldx, u, aq, as, M, K, mod, stream, il);
+    if (group == 128) return launch_rot_quant<ACT, I4, 128>(x, ldx, u, aq, as, M, K, mod, stream, il);
     return RDA_ERR_INVALID;
 }
 
@@ -349,6 +357,10 @@ int rda_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, 
 
 int rda_rot_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
     return dispatch_group<NO_ACT, false>(group, x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream);
+}
+
+int rda_rot_quant_pack_a_il(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {
+    return dispatch_group<NO_ACT, false>(group, x, ldx, nullptr, a_q, a_scale, M, K, ModArgs{}, stream, 1);
 }
 
 int rda_situ_rot_quant_pack_a(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream) {

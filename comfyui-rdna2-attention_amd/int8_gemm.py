@@ -31,7 +31,7 @@ MAX_ROT_K = 16384  # Keeps the rotated row within the LDS of a workgroup.
 ROT_GROUP = 256
 
 KERNELS = ("quant_pack_a", "rot_quant_pack_a", "situ_rot_quant_pack_a", "swiglu_rot_quant_pack_a", "gate_rot_quant_pack_a", "mod_rot_quant_pack_a",
-           "rot_quant_pack_a_i4", "gemm", "gemm_i4", "gemm_w4a8", "gemm_acc")
+           "rot_quant_pack_a_i4", "gemm", "gemm_i4", "gemm_w4a8", "gemm_acc", "rot_quant_pack_a_il", "gemm_w4a8_il")
 
 kernels = None
 # The functions and classes the hooks replace, saved the first time enable() runs.
@@ -127,20 +127,34 @@ def linear(x, weight, weight_scale, bias, rotate=False, situ=False, up=None, gat
     return run(quant, k.gemm, x, weight, weight_scale, bias, weight.shape[1], up if gate is None else gate, activations, res, group)
 
 
+def _interleaved(qweight, group_scales, bias, N, K, rotate, scale_group):
+    """Whether a W4A8 linear can run on k-interleaved activations (each 8 values of k as their 4 even ones, then their 4
+    odd ones: the order in which the GEMM widens packed int4, so it needs no byte interleave). That GEMM is the
+    direct-copy kernel only: 128-wide scale groups, K and N multiples of 128, the weight and scales on 16-byte and the
+    bias on 8-byte boundaries, and K within the rotated rows a workgroup holds."""
+    return (rotate and scale_group == 128 and K % 128 == 0 and N % 128 == 0 and K <= MAX_ROT_K and qweight.data_ptr() % 16 == 0
+            and group_scales.data_ptr() % 16 == 0 and (bias is None or bias.data_ptr() % 8 == 0))
+
+
 def linear_w4a8(x, qweight, group_scales, bias=None, rotate=True, group=ROT_GROUP, scale_group=128, activations=None):
     """W4A8: x (M, K) fp16 is rotated (group-size blocks) and quantized per token to int8; qweight (N, K/2) signed int4,
-    two per byte, low nibble first; group_scales (N, K / scale_group) fp16. Returns (M, N) fp16."""
+    two per byte, low nibble first; group_scales (N, K / scale_group) fp16. activations, if given, are x already
+    quantized by rot_quant_pack_a (or quant_pack_a) in natural order. Returns (M, N) fp16."""
     k = get_kernels()
     M, K = x.shape
     N = qweight.shape[0]
     if M == 0 or N == 0:
         return torch.empty((M, N), dtype=torch.float16, device=x.device)
+    gemm = k.gemm_w4a8
     if activations is None:
-        activations = quantize(k.rot_quant_pack_a if rotate else k.quant_pack_a, x, K, None, group)
+        if _interleaved(qweight, group_scales, bias, N, K, rotate, scale_group):
+            activations, gemm = quantize(k.rot_quant_pack_a_il, x, K, None, group), k.gemm_w4a8_il
+        else:
+            activations = quantize(k.rot_quant_pack_a if rotate else k.quant_pack_a, x, K, None, group)
     packed_a, a_scale = activations
     out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     p = _lib.ptr
-    launch(k.gemm_w4a8, 0, 0, 0, [p(packed_a), p(qweight), p(a_scale), p(group_scales), p(bias), p(out), M, N, K, scale_group])
+    launch(gemm, 0, 0, 0, [p(packed_a), p(qweight), p(a_scale), p(group_scales), p(bias), p(out), M, N, K, scale_group])
     return out
 
 

@@ -76,6 +76,17 @@ int rda_gemm_i4(const void* a_q, const void* w_packed, const float* a_scale, con
 int rda_gemm_w4a8(const void* a_q, const void* w_packed, const float* a_scale, const void* group_scales, const void* bias, void* c, int M, int N, int K,
                   int group, void* stream);
 
+/* W4A8 on k-interleaved activations (no reference counterpart; linear_w4a8's own quantize-then-GEMM pair):
+ * rda_rot_quant_pack_a_il writes the same int8 codes and scales as rda_rot_quant_pack_a, but each 8 values of k as
+ * its 4 even ones, then its 4 odd ones -- the order in which the GEMM widens packed int4 weights (low nibbles, then
+ * high ones), so that it needs no byte interleave; rda_gemm_w4a8_il takes those activations and gives rda_gemm_w4a8's
+ * outputs bit for bit. It takes only shapes its direct-copy kernel runs: group 128, K % 128 == 0, N % 128 == 0,
+ * K up to 40960 (the block's group scales are staged in LDS), a_q, w_packed, c and group_scales on 16-byte and bias
+ * on 8-byte boundaries (RDA_ERR_INVALID otherwise). */
+int rda_rot_quant_pack_a_il(const void* x, long ldx, void* a_q, float* a_scale, int M, int K, int group, void* stream);
+int rda_gemm_w4a8_il(const void* a_q, const void* w_packed, const float* a_scale, const void* group_scales, const void* bias, void* c, int M, int N,
+                     int K, int group, void* stream);
+
 /* Parity entry (no reference counterpart): the raw int32 accumulators [M, N] of the int8 x int8
  * (w_int4 = 0) or int8 x int4 (w_int4 = 1) product. */
 int rda_gemm_acc(const void* a_q, const void* w, int w_int4, void* acc, int M, int N, int K, void* stream);

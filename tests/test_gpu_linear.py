@@ -5,7 +5,7 @@ import pytest
 import torch
 
 import oracle
-from comfyui_rdna2_attention_amd import int8_gemm
+from comfyui_rdna2_attention_amd import _lib, int8_gemm
 from helpers import assert_same, activations, bits, channel_scales, gen, int4_weights, int8_weights, q_of
 
 pytestmark = pytest.mark.gpu
@@ -248,6 +248,49 @@ def test_w4a8_full_size_every_output(dev):
         y = total.float().double()
     ref = (y * a_scale.double()[:, None]).float().half()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"{(out != ref).sum().item()} outputs differ"
+
+
+# Shapes of each block the k-interleaved pair runs (two 128 x 128 blocks per CU; past K = 3456 one 128 x 256 block, or
+# one 128 x 128 block when N % 256 != 0), rotation groups 256 and 128, a partial last row block, with and without bias.
+@pytest.mark.parametrize("M,N,K,group,with_bias", [(520, 512, 1024, 256, False), (200, 256, 12288, 256, True), (300, 384, 8192, 128, False),
+                                                   (129, 128, 1280, 256, True), (64, 128, 128, 128, False)])
+def test_w4a8_interleaved_pair_matches_natural(dev, M, N, K, group, with_bias):
+    """rot_quant_pack_a_il writes rot_quant_pack_a's scales, and its codes with each 8 values of k as the 4 even ones,
+    then the 4 odd ones; gemm_w4a8_il on them (linear_w4a8's default route) gives gemm_w4a8's outputs on the natural
+    codes bit for bit."""
+    print(f"w4a8 interleaved M={M} N={N} K={K} group={group} bias={with_bias}", flush=True)
+    x = activations(M, K, seed=71, outliers=0).to(dev)
+    _, wp = int4_weights(N, K, seed=72)
+    gs = (torch.rand(N, K // 128, generator=gen(73)) * 1.5e-2 + 5e-3).half().to(dev)
+    bias = (torch.rand(N, generator=gen(74)) - 0.5).half().to(dev) if with_bias else None
+    wp = wp.to(dev)
+    k = kern()
+    assert int8_gemm._interleaved(wp, gs, bias, N, K, True, 128)
+    nat = int8_gemm.quantize(k.rot_quant_pack_a, x, K, group=group)
+    il = int8_gemm.quantize(k.rot_quant_pack_a_il, x, K, group=group)
+    assert torch.equal(il[1], nat[1])
+    qn = nat[0].view(torch.int8)[:M * K].view(M, K // 8, 8)
+    qi = il[0].view(torch.int8)[:M * K].view(M, K // 8, 8)
+    assert torch.equal(qi, torch.cat([qn[..., 0::2], qn[..., 1::2]], dim=-1))
+    out_nat = int8_gemm.linear_w4a8(x, wp, gs, bias, group=group, activations=nat)
+    out_il = int8_gemm.linear_w4a8(x, wp, gs, bias, group=group)
+    assert torch.equal(out_il.view(torch.int16), out_nat.view(torch.int16)), f"{(out_il != out_nat).sum().item()} outputs differ"
+
+
+def test_w4a8_interleaved_gemm_refuses_other_shapes(dev):
+    """gemm_w4a8_il serves only its direct-copy kernel: N % 128 != 0 and a 64-wide scale group are refused before any
+    launch, where linear_w4a8 keeps the natural-order pair."""
+    M, N, K = 64, 192, 256
+    a = torch.zeros(256 * K // 4, dtype=torch.int32, device=dev)
+    s = torch.ones(M, dtype=torch.float32, device=dev)
+    w = torch.zeros(N, K // 2, dtype=torch.int8, device=dev)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    p = _lib.ptr
+    for n, group, gs in ((N, 128, torch.ones(N, K // 128, dtype=torch.float16, device=dev)),
+                         (128, 64, torch.ones(128, K // 64, dtype=torch.float16, device=dev))):
+        with pytest.raises(RuntimeError, match="HIP error 1"):
+            _lib.call("rda_gemm_w4a8_il", p(a), p(w), p(s), p(gs), None, p(out), M, n, K, group)
+    assert not int8_gemm._interleaved(w, torch.ones(N, K // 128, dtype=torch.float16, device=dev), None, N, K, True, 128)
 
 
 def test_w4a4_hook_path_bit_exact(dev):
