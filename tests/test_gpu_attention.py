@@ -41,10 +41,11 @@ def close(out, ref):
 # twelve-wave workgroups (384 rows per workgroup over the (batch, head, row) range, each head's rows padded to a
 # multiple of 32): one head with padding rows (513); two whole heads; rows spanning heads with GQA 3:1 over two
 # batches and a partial last workgroup; spanning heads with GQA 2:1 and a partial last key tile; padded heads
-# spanning workgroups (400, 1000).
+# spanning workgroups (400, 1000); and 1, 2, 3, 4, 5, 7, 10, 33 and 128 key tiles.
 @pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096),
                                           (1, 2, 1, 200, 1049), (1, 1, 1, 64, 96), (1, 2, 2, 130, 150), (1, 1, 1, 129, 192), (2, 2, 1, 70, 210),
-                                          (1, 2, 2, 384, 100), (2, 3, 1, 416, 300), (1, 4, 2, 640, 1049), (1, 3, 3, 400, 300), (2, 2, 1, 1000, 77)])
+                                          (1, 2, 2, 384, 100), (2, 3, 1, 416, 300), (1, 4, 2, 640, 1049), (1, 3, 3, 400, 300), (2, 2, 1, 1000, 77),
+                                          (1, 2, 2, 384, 20), (1, 1, 1, 400, 40), (1, 2, 1, 384, 224), (1, 1, 1, 500, 160)])
 def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
     print(f"attention B={B} H={H} Hkv={Hkv} Lq={Lq} Lk={Lk} int8_qk={int8_qk}", flush=True)
     q, k, v = qkv(B, H, Hkv, Lq, Lk, seed=Lq + Lk)
