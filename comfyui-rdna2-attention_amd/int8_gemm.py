@@ -96,9 +96,41 @@ def quantize(quant, x, K, up=None, group=ROT_GROUP):
     return packed_a, a_scale
 
 
+def _check_linear(what, x, x_cols, K, weight, weight_dtypes, row_bytes, scales, n_scales, scales_dtype, bias, activations, up=None):
+    """Raises ValueError unless the tensors have the shapes, dtypes and layouts the kernels read: x (M, x_cols) fp16 (and
+    up, if given, M x K fp16 values); a contiguous weight (N, row_bytes); contiguous scales of n_scales values; bias None or N
+    contiguous fp16 values; activations, if given, holding M rows of K codes and M fp32 scales. (The kernels trust
+    these sizes.)"""
+    if x.dim() != 2 or x.dtype != torch.float16 or x.shape[1] != x_cols:
+        raise ValueError(f"{what} takes x as (M, {x_cols}) fp16, not {tuple(x.shape)} {x.dtype}")
+    if up is not None and (up.dtype != torch.float16 or up.numel() != x.shape[0] * K):
+        raise ValueError(f"{what} takes its second input as {x.shape[0]} x {K} fp16 values, not {tuple(up.shape)} {up.dtype}")
+    if weight.dim() != 2 or weight.dtype not in weight_dtypes or weight.shape[1] != row_bytes or not weight.is_contiguous():
+        raise ValueError(f"{what} takes a contiguous (N, {row_bytes}) weight of {' or '.join(str(d) for d in weight_dtypes)}")
+    N = weight.shape[0]
+    if scales.dtype != scales_dtype or scales.numel() != n_scales or not scales.is_contiguous():
+        raise ValueError(f"{what}: the weight scales must be {n_scales} contiguous {scales_dtype} values")
+    if bias is not None and (bias.dtype != torch.float16 or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError(f"{what}: bias must be {N} contiguous fp16 values")
+    if activations is not None:
+        packed_a, a_scale = activations
+        M = x.shape[0]
+        if packed_a.numel() * packed_a.element_size() < M * K or a_scale.dtype != torch.float32 or a_scale.numel() < M:
+            raise ValueError(f"{what}: activations must hold {M} rows of {K} codes and {M} fp32 scales")
+
+
 def run(quant, gemm, x, weight, weight_scale, bias, K, up=None, activations=None, res=None, group=ROT_GROUP):
     """K is the number of values per row. weight is (N, row_bytes) int8 (row_bytes = K, or K / 2 for packed int4)
     and weight_scale (N,) fp32. Returns (M, N) fp16."""
+    k = get_kernels()
+    int4 = gemm is k.gemm_i4
+    _check_linear("run", x, 2 * K if quant is k.situ_rot_quant_pack_a else K, K, weight, (torch.int8, torch.uint8) if int4 else (torch.int8,),
+                  K // 2 if int4 else K, weight_scale, weight.shape[0] if weight.dim() == 2 else -1, torch.float32, bias, activations, up)
+    return _run(quant, gemm, x, weight, weight_scale, bias, K, up, activations, res, group)
+
+
+def _run(quant, gemm, x, weight, weight_scale, bias, K, up, activations, res, group):
+    """run() on arguments already checked."""
     k = get_kernels()
     M = x.shape[0]
     N = weight.shape[0]
@@ -121,10 +153,14 @@ def run(quant, gemm, x, weight, weight_scale, bias, K, up=None, activations=None
 def linear(x, weight, weight_scale, bias, rotate=False, situ=False, up=None, gate=None, activations=None, res=None, group=ROT_GROUP):
     """x is (M, K) fp16, or (M, 2K) with situ, weight (N, K) int8 and weight_scale (N,) fp32. With up, x is the gate of a SwiGLU.
     With gate, x is multiplied by its sigmoid. Returns (M, N) fp16."""
+    K = weight.shape[1] if weight.dim() == 2 else -1
+    second = up if gate is None else gate
+    _check_linear("linear", x, 2 * K if situ and second is None else K, K, weight, (torch.int8,), K, weight_scale,
+                  weight.shape[0] if weight.dim() == 2 else -1, torch.float32, bias, activations, second)
     k = get_kernels()
     quant = (k.gate_rot_quant_pack_a if gate is not None else k.swiglu_rot_quant_pack_a if up is not None else k.situ_rot_quant_pack_a if situ
              else k.rot_quant_pack_a if rotate else k.quant_pack_a)
-    return run(quant, k.gemm, x, weight, weight_scale, bias, weight.shape[1], up if gate is None else gate, activations, res, group)
+    return _run(quant, k.gemm, x, weight, weight_scale, bias, K, second, activations, res, group)
 
 
 def _interleaved(qweight, group_scales, bias, N, K, rotate, scale_group):
@@ -140,9 +176,13 @@ def linear_w4a8(x, qweight, group_scales, bias=None, rotate=True, group=ROT_GROU
     """W4A8: x (M, K) fp16 is rotated (group-size blocks) and quantized per token to int8; qweight (N, K/2) signed int4,
     two per byte, low nibble first; group_scales (N, K / scale_group) fp16. activations, if given, are x already
     quantized by rot_quant_pack_a (or quant_pack_a) in natural order. Returns (M, N) fp16."""
-    k = get_kernels()
+    if x.dim() != 2 or x.shape[1] % scale_group or x.shape[1] % 2:
+        raise ValueError(f"linear_w4a8 takes x as (M, K) with K a multiple of {scale_group} and of 2, not {tuple(x.shape)}")
     M, K = x.shape
-    N = qweight.shape[0]
+    N = qweight.shape[0] if qweight.dim() == 2 else -1
+    _check_linear("linear_w4a8", x, K, K, qweight, (torch.int8, torch.uint8), K // 2, group_scales, N * (K // scale_group), torch.float16, bias,
+                  activations)
+    k = get_kernels()
     if M == 0 or N == 0:
         return torch.empty((M, N), dtype=torch.float16, device=x.device)
     gemm = k.gemm_w4a8

@@ -586,3 +586,31 @@ def test_gemv_wrappers_check_their_inputs():
             int8_gemv.gemv_multi(torch.zeros(512), [(w, bad_scale, bad_bias)])
     with pytest.raises(ValueError):
         int8_gemv.gemv(torch.zeros(512), w.t().contiguous().t(), s)  # a transposed (non-contiguous) weight
+
+
+def test_gemm_wrappers_check_their_inputs():
+    """linear / run and linear_w4a8 refuse tensors the kernels would read past or misread (a weight of the wrong width,
+    dtype or layout, scales or a bias of the wrong length or dtype, an x of the wrong width, too small activations)
+    before any allocation on the device or launch."""
+    M, N, K = 8, 64, 256
+    x, w, ws = torch.zeros(M, K, dtype=torch.float16), torch.zeros(N, K, dtype=torch.int8), torch.ones(N)
+    bad_linear = [dict(x=x.float()), dict(x=torch.zeros(M, K + 16, dtype=torch.float16)), dict(weight=torch.zeros(N, K - 16, dtype=torch.int8)),
+                  dict(weight=w.to(torch.uint8)), dict(weight=torch.zeros(K, N, dtype=torch.int8).t()), dict(weight_scale=ws.half()),
+                  dict(weight_scale=torch.ones(N - 1)), dict(bias=torch.zeros(N)), dict(bias=torch.zeros(N - 1, dtype=torch.float16)),
+                  dict(activations=(torch.zeros(M * K // 8, dtype=torch.int32), torch.ones(M)))]
+    for bad in bad_linear:
+        args = dict(x=x, weight=w, weight_scale=ws, bias=None, activations=None) | bad
+        with pytest.raises(ValueError):
+            int8_gemm.linear(args["x"], args["weight"], args["weight_scale"], args["bias"], rotate=True, activations=args["activations"])
+    with pytest.raises(ValueError):  # SwiGLU: the up projection must match the gate
+        int8_gemm.linear(x, w, ws, None, up=torch.zeros(M, K // 2, dtype=torch.float16))
+    with pytest.raises(ValueError):  # situ reads rows of 2K values
+        int8_gemm.linear(x, w, ws, None, situ=True)
+    w4, gs = torch.zeros(N, K // 2, dtype=torch.uint8), torch.ones(N, K // 128, dtype=torch.float16)
+    bad_w4a8 = [dict(x=torch.zeros(M, K + 64, dtype=torch.float16)), dict(qweight=torch.zeros(N, K, dtype=torch.uint8)),
+                dict(group_scales=gs.float()), dict(group_scales=torch.ones(N, K // 64, dtype=torch.float16)),
+                dict(group_scales=torch.ones(K // 128, N, dtype=torch.float16).t()), dict(bias=torch.zeros(N))]
+    for bad in bad_w4a8:
+        args = dict(x=x, qweight=w4, group_scales=gs, bias=None) | bad
+        with pytest.raises(ValueError):
+            int8_gemm.linear_w4a8(args["x"], args["qweight"], args["group_scales"], args["bias"])
