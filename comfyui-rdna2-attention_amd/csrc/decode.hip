@@ -591,7 +591,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     __shared__ float max_s[W][REP], sum_s[W][REP];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, pos = lane >> 4, sub = lane & 15;
     const int b = blockIdx.y / kv_heads, kv_head = blockIdx.y % kv_heads, split = blockIdx.x;
-    const int length = lengths[b];
+    const int length = min(max(lengths[b], 0), capacity);  // a length past the cache reads no row beyond it
     const int chunk = (length + SPLITS - 1) / SPLITS;
     const int begin = split * chunk, end = min(begin + chunk, length);
     const int first_head = (b * kv_heads + kv_head) * REP;

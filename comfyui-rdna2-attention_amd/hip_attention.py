@@ -55,8 +55,10 @@ def attention(q, k, v, out, scale, int8_qk=False):
     if kernels is None:
         kernels = Kernels("hip_attention", ("attn", "pack_k_i8", "attn_i8", "attn_i8_workspace"))
     for t in (q, k, v, out):
-        if t.dtype != torch.float16 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1 or not t.is_cuda:
+        if t.dim() != 4 or t.dtype != torch.float16 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1 or not t.is_cuda:
             raise ValueError("attention expects (B, H, L, 128) fp16 GPU tensors with a contiguous last dimension")
+    if out.shape != q.shape or v.shape != k.shape or k.shape[0] != q.shape[0] or k.shape[1] == 0 or q.shape[1] % k.shape[1]:
+        raise ValueError("attention expects out shaped as q, v as k, one batch size, and q's heads a multiple of k's")
     b, heads, q_len, _ = q.shape
     _, kv_heads, k_len, _ = k.shape
     if out.numel() == 0:  # nothing to compute (the kernels reject empty shapes)

@@ -316,9 +316,18 @@ def logits(transformer, x):
 
 
 def attention_decode(q, k, v, lengths):
-    """q is (batch, 1, heads, 128), k and v are (batch, capacity, kv heads, 128) and lengths (batch,) int32, all but lengths fp32."""
+    """q is (batch, 1, heads, 128), k and v are (batch, capacity, kv heads, 128) and lengths (batch,) int32, all but lengths fp32.
+    Lengths are read on the device (a captured graph stays valid as the cache grows); one past capacity counts as
+    capacity."""
+    if q.dim() != 4 or k.dim() != 4 or q.shape[1] != 1 or q.shape[3] != HEAD or k.shape[3] != HEAD or v.shape != k.shape:
+        raise ValueError("attention_decode takes q (batch, 1, heads, 128) and k, v (batch, capacity, kv heads, 128)")
     batch, _, heads, _ = q.shape
     _, capacity, kv_heads, _ = k.shape
+    if (k.shape[0] != batch or kv_heads == 0 or heads % kv_heads or heads // kv_heads not in (1, 2, 4, 8)
+            or any(t.dtype != torch.float32 for t in (q, k, v)) or not (k.is_contiguous() and v.is_contiguous())
+            or lengths.dtype != torch.int32 or lengths.numel() != batch):
+        raise ValueError("attention_decode takes fp32 q and contiguous fp32 k, v of one batch size, 1, 2, 4 or 8 query heads per "
+                         "kv head, and int32 lengths, one per batch row")
     k_ = get_kernels()
     q = q.contiguous()
     out = torch.empty_like(q)

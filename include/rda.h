@@ -144,7 +144,7 @@ int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const voi
 int rda_gemv_bf16(const float* x, const void* w, float* out, int N, int K, void* stream);
 
 /* attn_decode, int8_gemv.py:111-112 (int8_gemv.hip:121-180): q (B, 1, H, 128), k/v (B, capacity,
- * Hkv, 128) fp32, lengths (B,) int32 read on the device; partial (B*H, splits, 128) and stats
+ * Hkv, 128) fp32, lengths (B,) int32 read on the device (one past capacity counts as capacity); partial (B*H, splits, 128) and stats
  * (B*H, splits, 2) fp32 with splits = rda_decode_splits(). H / Hkv in {1, 2, 4, 8}. */
 int rda_attn_decode(const float* q, const float* k, const float* v, const int* lengths, float* partial, float* stats, int B, int H, int Hkv,
                     int capacity, float scale, void* stream);

@@ -140,6 +140,17 @@ def test_attention_decode(dev, B, H, Hkv, cap, lengths):
     assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
 
 
+def test_attention_decode_length_past_capacity(dev):
+    """A length past the cache's capacity reads no row beyond it: the kernel takes it as the capacity, bit for bit."""
+    g = gen(23)
+    q = torch.randn(2, 1, 8, 128, generator=g).to(dev)
+    k = torch.randn(2, 96, 2, 128, generator=g).to(dev)
+    v = torch.randn(2, 96, 2, 128, generator=g).to(dev)
+    past = int8_gemv.attention_decode(q, k, v, torch.tensor([97, 5000], dtype=torch.int32, device=dev))
+    full = int8_gemv.attention_decode(q, k, v, torch.tensor([96, 96], dtype=torch.int32, device=dev))
+    assert torch.equal(past.view(torch.int32), full.view(torch.int32))
+
+
 # D > 128: one wave per row, 1-4 steps per slot (D = 136 .. 8192, chunk counts that leave slots and steps partly or
 # wholly empty), row counts that leave a workgroup's last waves without a row; D <= 128: 16 lanes per row.
 @pytest.mark.parametrize("shape", [(1, 4096, 3072), (2, 3, 50, 128), (1, 7, 64), (1, 5, 8192), (2, 9, 136), (1, 3, 5120), (3, 2, 2048),

@@ -614,3 +614,17 @@ def test_gemm_wrappers_check_their_inputs():
         args = dict(x=x, qweight=w4, group_scales=gs, bias=None) | bad
         with pytest.raises(ValueError):
             int8_gemm.linear_w4a8(args["x"], args["qweight"], args["group_scales"], args["bias"])
+
+
+def test_decode_attention_checks_its_inputs():
+    """attention_decode refuses what its kernels would misread or read past -- a cache of another dtype or layout, v
+    shaped unlike k, heads not a multiple of the KV heads, lengths not one int32 per batch row -- before any launch."""
+    q, k = torch.zeros(2, 1, 8, 128), torch.zeros(2, 64, 2, 128)
+    ln = torch.full((2,), 64, dtype=torch.int32)
+    bad = [dict(k=k.half(), v=k.half()), dict(v=torch.zeros(2, 32, 2, 128)), dict(q=torch.zeros(2, 1, 7, 128)), dict(q=torch.zeros(2, 1, 6, 128)),
+           dict(k=k.transpose(1, 2).contiguous().transpose(1, 2), v=k.transpose(1, 2).contiguous().transpose(1, 2)),
+           dict(lengths=ln.long()), dict(lengths=ln[:1]), dict(q=torch.zeros(2, 1, 8, 64)), dict(q=torch.zeros(3, 1, 8, 128))]
+    for b in bad:
+        args = dict(q=q, k=k, v=k.clone(), lengths=ln) | b
+        with pytest.raises(ValueError):
+            int8_gemv.attention_decode(args["q"], args["k"], args["v"], args["lengths"])
