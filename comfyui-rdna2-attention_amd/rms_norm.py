@@ -36,6 +36,9 @@ def _weight_fp32(scale, device):
 
 def rms_norm(x, weight, eps):
     """x is (B, L, D) or (B, H, L, D) fp16 with a contiguous last dimension, weight (D,) fp32 and zero-centered. Returns contiguous fp16."""
+    if not eligible(x) or weight.dtype != torch.float32 or weight.numel() != x.shape[-1] or not weight.is_contiguous():
+        raise ValueError("rms_norm takes (B, L, D) or (B, H, L, D) fp16 with a contiguous last dimension (D a multiple of 8, "
+                         f"at most {MAX_DIM}) and D contiguous fp32 weights")
     k = get_kernels()
     rows = x if x.ndim == 4 else x.unsqueeze(1)
     B, H, L, D = rows.shape
@@ -51,11 +54,18 @@ def rms_norm(x, weight, eps):
 
 def rms_norm_rope(x, heads, module, freqs):
     """x is (B, L, heads * 128) fp16 and freqs (B or 1, 1, L, 64, 2, 2) fp32. Returns (B, heads, L, 128) with QK-norm and rope applied."""
+    if x.dim() != 3 or x.dtype != torch.float16 or x.shape[2] != heads * HEAD_DIM or x.stride(2) != 1:
+        raise ValueError(f"rms_norm_rope takes x as (B, L, {heads} x {HEAD_DIM}) fp16 with a contiguous last dimension")
     B, L, _ = x.shape
+    if (freqs.dtype != torch.float32 or not freqs.is_contiguous() or freqs.shape[0] not in (1, B)
+            or freqs.numel() != freqs.shape[0] * L * HEAD_DIM * 2):
+        raise ValueError(f"rms_norm_rope takes contiguous fp32 freqs of shape (1 or {B}, 1, {L}, 64, 2, 2)")
     out = torch.empty((B, heads, L, HEAD_DIM), dtype=x.dtype, device=x.device)
     if out.numel() == 0:
         return out
     weight = _weight_fp32(module.scale, x.device)
+    if weight.numel() != HEAD_DIM or not weight.is_contiguous():
+        raise ValueError(f"rms_norm_rope takes {HEAD_DIM} norm weights")
     batch_stride = L * HEAD_DIM // 2 if freqs.shape[0] > 1 else 0
     p = _lib.ptr
     launch(get_kernels().rms_norm_rope, 0, 0, THREADS, [p(x), p(weight), p(out), B, heads, L, HEAD_DIM, x.stride(0), HEAD_DIM, x.stride(1),

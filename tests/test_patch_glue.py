@@ -628,3 +628,16 @@ def test_decode_attention_checks_its_inputs():
         args = dict(q=q, k=k, v=k.clone(), lengths=ln) | b
         with pytest.raises(ValueError):
             int8_gemv.attention_decode(args["q"], args["k"], args["v"], args["lengths"])
+
+
+def test_rms_norm_wrappers_check_their_inputs():
+    """rms_norm and rms_norm_rope refuse weights, frequencies and inputs whose sizes the kernels would read past."""
+    x = torch.zeros(1, 4, 256, dtype=torch.float16)
+    for bad in ((x.float(), torch.zeros(256)), (x, torch.zeros(128)), (x, torch.zeros(256, dtype=torch.float16)), (x[..., :250], torch.zeros(250))):
+        with pytest.raises(ValueError):
+            rms_norm.rms_norm(*bad, 1e-6)
+    norm = types.SimpleNamespace(scale=torch.zeros(128), eps=1e-6)
+    q, f = torch.zeros(2, 4, 256, dtype=torch.float16), torch.zeros(1, 1, 4, 64, 2, 2)
+    for bad in ((q, 3, f), (q.float(), 2, f), (q, 2, torch.zeros(1, 1, 3, 64, 2, 2)), (q, 2, f.double()), (q, 2, torch.zeros(3, 1, 4, 64, 2, 2))):
+        with pytest.raises(ValueError):
+            rms_norm.rms_norm_rope(bad[0], bad[1], norm, bad[2])
