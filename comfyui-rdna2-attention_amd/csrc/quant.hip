@@ -103,16 +103,19 @@ __device__ __forceinline__ int cvt_floor(float x) {
     return r;
 }
 
+// The low bytes of a, b, c, d as one word (a in the lowest byte): three byte permutes.
 __device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
-    return (u32)(a & 255) | ((u32)(b & 255) << 8) | ((u32)(c & 255) << 16) | ((u32)(d & 255) << 24);
+    const u32 ab = __builtin_amdgcn_perm((u32)b, (u32)a, 0x0c0c0400u), cd = __builtin_amdgcn_perm((u32)d, (u32)c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
 // GROUP 256 or 128 rotates; GROUP 0 is quant_pack_a (no rotation, int8_gemm.hip:93-103). NW waves per row: the
 // launcher sizes it to the row (K / 1024 waves, so that K = 3072 keeps every lane busy in both passes: the kernel
 // is vector-ALU bound); MOD keeps 4 (QT threads), whose sum of squares follows the reference's thread order.
-template <int ACT, bool I4, int GROUP, int NW>
+// IL: the codes k-interleaved (each 8 values of k stored as their 4 even ones, then their 4 odd ones).
+template <int ACT, bool I4, int GROUP, int NW, bool IL>
 __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
-                                                       int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod, int interleave) {
+                                                       int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ float red[8];
     half_t* rotated = (half_t*)smem;
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
             else q[i] = cvt_floor(fminf(fmaxf(d + 0.5f, -128.f), 127.f));
         }
         u4v o;
-        if (interleave) {  // k-interleaved: each 8 values of k as its 4 even ones, then its 4 odd ones
+        if constexpr (IL) {
 #pragma unroll
             for (int d = 0; d < 4; d++) {
                 const int b = (d >> 1) * 8 + (d & 1);
@@ -318,8 +321,15 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
 template <int ACT, bool I4, int GROUP, int NW>
 static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream, int il) {
     const size_t lds = GROUP ? (size_t)K * 2 + NW * 64 * 17 * sizeof(float) : K <= MAX_LDS_K ? (size_t)K * 2 : 0;
-    hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
-                       (const half_t*)u, (int8_t*)aq, as, K, mod, il);
+    if (il) {  // k-interleaved codes: the plain rotation only
+        if constexpr (ACT == NO_ACT && !I4 && GROUP != 0)
+            hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW, true>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
+                               (const half_t*)u, (int8_t*)aq, as, K, mod);
+        else return RDA_ERR_INVALID;
+    } else {
+        hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW, false>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
+                           (const half_t*)u, (int8_t*)aq, as, K, mod);
+    }
     return (int)hipGetLastError();
 }
 
