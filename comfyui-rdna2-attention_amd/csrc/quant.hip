@@ -293,11 +293,19 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
     const h8* src = staged ? (const h8*)rotated : (const h8*)x;
     for (int ch = t; ch < K / 16; ch += NW * 64) {
         const h8 lo = src[ch * 2], hi = src[ch * 2 + 1];
+        const u4v wl = __builtin_bit_cast(u4v, lo), wh = __builtin_bit_cast(u4v, hi);
         int q[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const float f = (float)(i < 8 ? lo[i] : hi[i - 8]);
-            const float d = div_by_scale(f, scale, rcp);  // f / scale
+            // f / scale as div_by_scale, its first product f * rcp taken straight from the fp16 value (one mixed-precision
+            // FMA, + 0, in place of a conversion and a multiply: the same value, up to the sign of a zero, which the
+            // code does not depend on).
+            const u32 w = i < 8 ? wl[i >> 1] : wh[(i - 8) >> 1];
+            float y;
+            if (i & 1) asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(y) : "v"(w), "v"(rcp));
+            else asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(w), "v"(rcp));
+            const float d = __builtin_fmaf(__builtin_fmaf(-y, scale, f), rcp, y);
             // int8_gemm.hip:84 and :53. The clamp to [lo, hi] (integers) goes before the rounding: both orders give the same
             // code for every input, NaN included (-128 / -7), and floor then truncation fuse into one conversion.
             if (I4) q[i] = (int)rintf(fminf(fmaxf(d, -7.f), 7.f));
