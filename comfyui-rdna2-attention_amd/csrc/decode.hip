@@ -578,15 +578,26 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_bf16_kernel(const float* _
 
 // attn_decode (int8_gemv.hip:121-180): one new token over the cache, split by position so that a few
 // KV heads still fill the GPU. The grid is fixed and the length is read here, so a captured graph
-// stays valid as the cache grows. Memory-level parallelism is the point: a wave takes 16 positions at
-// once (16 lanes per position, 8 dims per lane), issues all their K and V loads before any arithmetic,
-// then folds the 16 scores of each query head into its running (max, sum, acc) with one rescale. The
-// REP query heads of the KV head share every load.
+// stays valid as the cache grows. Memory-level parallelism is the point: a wave takes 4 ITS positions at
+// once (16 lanes per position, 8 dims per lane), issues all their K and V loads (non-temporal: the cache is
+// read once per token) before any arithmetic, then folds the scores of each query head into its running
+// (max, sum, acc) with one rescale per half. The REP query heads of the KV head share every load.
+// Per REP, as measured (decode + merge, graph-replayed, B = 1, 2048 positions): one query head per KV head
+// takes eight waves of 8 positions (9.9 -> 8.0 us), the others four waves of 16; the q.k and p.v products are
+// FMA chains up to four heads (REP 2: 10.7 -> 8.6 us, REP 4: 10.1 -> 9.4 us) and separate multiplies and adds
+// at eight (13.5 -> 13.0 us; with FMA chains, 13.5: more registers than the rescale schedule keeps).
 template <int REP>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-                                                          const int* __restrict__ lengths, float* __restrict__ partial, float* __restrict__ stats,
-                                                          int capacity, int kv_heads, float scale) {
-    constexpr int W = 4, ITS = 4, PW = 4 * ITS;  // waves; 4-position steps per round; positions per wave per round
+struct DecodeShape {
+    static constexpr int W = REP == 1 ? 8 : 4, ITS = REP == 1 ? 2 : 4;  // waves; 4-position steps per round
+    static constexpr bool FMA = REP <= 4;
+};
+template <int REP>
+__global__ __launch_bounds__(DecodeShape<REP>::W * 64) void attn_decode_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                                              const float* __restrict__ v, const int* __restrict__ lengths,
+                                                                              float* __restrict__ partial, float* __restrict__ stats, int capacity,
+                                                                              int kv_heads, float scale) {
+    constexpr int W = DecodeShape<REP>::W, ITS = DecodeShape<REP>::ITS, PW = 4 * ITS;  // positions per wave per round
+    constexpr bool FMA = DecodeShape<REP>::FMA;
     __shared__ float acc_s[W][REP][HEAD];
     __shared__ float max_s[W][REP], sum_s[W][REP];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, pos = lane >> 4, sub = lane & 15;
@@ -611,8 +622,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
     for (int base = begin + wave * PW; base < end; base += W * PW) {
         f4 kr[ITS][2], vr[ITS][2];
         bool valid[ITS];
-        // Loads in the order the two halves of the round use them (K then V of steps 0-1, then of steps 2-3), so the
-        // first half's arithmetic waits only for its own data and runs while the second half's arrives.
+        // Loads in the order the two halves of the round use them (K then V of the first half's steps, then of the
+        // second half's), so the first half's arithmetic waits only for its own data and runs while the second half's
+        // arrives.
 #pragma unroll
         for (int half = 0; half < 2; half++) {
 #pragma unroll
@@ -620,15 +632,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
                 const int j = base + it * 4 + pos;
                 valid[it] = j < end;
                 const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
-                kr[it][0] = *(const f4*)(k + row);
-                kr[it][1] = *(const f4*)(k + row + 4);
+                kr[it][0] = __builtin_nontemporal_load((const f4*)(k + row));
+                kr[it][1] = __builtin_nontemporal_load((const f4*)(k + row + 4));
             }
 #pragma unroll
             for (int it = half * ITS / 2; it < (half + 1) * ITS / 2; it++) {
                 const int j = base + it * 4 + pos;
                 const size_t row = ((size_t)(b * capacity + (valid[it] ? j : base)) * kv_heads + kv_head) * HEAD + sub * 8;
-                vr[it][0] = *(const f4*)(v + row);
-                vr[it][1] = *(const f4*)(v + row + 4);
+                vr[it][0] = __builtin_nontemporal_load((const f4*)(v + row));
+                vr[it][1] = __builtin_nontemporal_load((const f4*)(v + row + 4));
             }
         }
 #pragma unroll
@@ -641,8 +653,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
 #pragma unroll
                 for (int u = 0; u < HI; u++) {
                     const int it = half * HI + u;
-                    const f4 d = qv[g][0] * kr[it][0] + qv[g][1] * kr[it][1];
-                    const float x = row_sum16((d[0] + d[1]) + (d[2] + d[3]));
+                    float x;
+                    if constexpr (FMA) {  // two chains of four
+                        float e0 = qv[g][0][0] * kr[it][0][0], e1 = qv[g][0][1] * kr[it][0][1];
+                        e0 = __builtin_fmaf(qv[g][0][2], kr[it][0][2], e0);
+                        e1 = __builtin_fmaf(qv[g][0][3], kr[it][0][3], e1);
+                        e0 = __builtin_fmaf(qv[g][1][0], kr[it][1][0], e0);
+                        e1 = __builtin_fmaf(qv[g][1][1], kr[it][1][1], e1);
+                        e0 = __builtin_fmaf(qv[g][1][2], kr[it][1][2], e0);
+                        e1 = __builtin_fmaf(qv[g][1][3], kr[it][1][3], e1);
+                        x = row_sum16(e0 + e1);
+                    } else {
+                        const f4 d = qv[g][0] * kr[it][0] + qv[g][1] * kr[it][1];
+                        x = row_sum16((d[0] + d[1]) + (d[2] + d[3]));
+                    }
                     s[u] = valid[it] ? x : -1e30f;
                     top = fmaxf(top, s[u]);
                 }
@@ -655,8 +679,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
                     const int it = half * HI + u;
                     const float p = valid[it] ? __expf(s[u] - next) : 0.f;
                     psum += p;
-                    a0 += vr[it][0] * p;
-                    a1 += vr[it][1] * p;
+                    if constexpr (FMA) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            a0[e] = __builtin_fmaf(vr[it][0][e], p, a0[e]);
+                            a1[e] = __builtin_fmaf(vr[it][1][e], p, a1[e]);
+                        }
+                    } else {
+                        a0 += vr[it][0] * p;
+                        a1 += vr[it][1] * p;
+                    }
                 }
                 psum = rows_sum(psum);
                 sum[g] = sum[g] * keep + psum;
@@ -684,7 +716,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restric
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < REP * HEAD; i += 256) {
+    for (int i = threadIdx.x; i < REP * HEAD; i += W * 64) {
         const int g = i / HEAD, d = i % HEAD;
         float top = max_s[0][g];
 #pragma unroll
@@ -933,10 +965,10 @@ int rda_attn_decode(const float* q, const float* k, const float* v, const int* l
     const int rep = H / Hkv;
     dim3 grid(SPLITS, B * Hkv);
     switch (rep) {
-    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
-    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
-    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
-    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(256), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 1: hipLaunchKernelGGL(attn_decode_kernel<1>, grid, dim3(DecodeShape<1>::W * 64), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 2: hipLaunchKernelGGL(attn_decode_kernel<2>, grid, dim3(DecodeShape<2>::W * 64), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 4: hipLaunchKernelGGL(attn_decode_kernel<4>, grid, dim3(DecodeShape<4>::W * 64), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
+    case 8: hipLaunchKernelGGL(attn_decode_kernel<8>, grid, dim3(DecodeShape<8>::W * 64), 0, (hipStream_t)stream, q, k, v, lengths, partial, stats, capacity, Hkv, scale); break;
     default: return RDA_ERR_INVALID;
     }
     return (int)hipGetLastError();
