@@ -394,24 +394,26 @@ struct GemvTable {
     int count;
 };
 
-// The rows of matrix `mi` in block `blk` of its range, with S waves per row (S = 1: RW rows per wave, rows
-// r GI_WAVES + wave of the block's RW GI_WAVES) and GW steps of 1024 per wave at most (steps past K / 1024 / S re-read
-// an in-bounds chunk and are skipped). XS: float4s (fp16: 4-vectors) of x per thread without the rotation; RS: sets
-// of 16 values per thread with it.
+// The rows of matrix `mi` in block `blk` of its range, with S waves per row and RW rows per wave (row
+// r GI_WAVES / S + wave / S of the block's RW GI_WAVES / S, part wave % S) and GW steps of 1024 per wave at most
+// (steps past K / 1024 / S re-read an in-bounds chunk and are skipped). Split matrices take RW = S, so that every
+// block holds GI_WAVES rows and each wave G loads, as a one-row-per-wave block does: a block rotates x once for 8
+// rows rather than for 8 / S (q|k|v, K = 4096: 1536 -> 768 blocks). XS: float4s (fp16: 4-vectors) of x per thread
+// without the rotation; RS: sets of 16 values per thread with it.
 template <int GW, int S, int RW, bool TAIL, bool XH, bool ROT, int XS, int RS>
 __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, const GemvTable& t, int mi, int blk, int K, int group,
                                                 float* __restrict__ rot_out, f4* xs, float* part_s) {
-    static_assert(S == 1 || RW == 1, "split rows take one row per wave group");
     constexpr int RPB = GI_WAVES / S * RW;
     const int steps = K / 1024, wsteps = steps / S;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row0 = blk * RPB + wave / S, part = wave % S;
     const int N = t.n[mi];
+    auto row_of = [&](int r) { return row0 + r * (GI_WAVES / S); };
     bool active[RW];
     const int8_t* base[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        const int row = row0 + r * GI_WAVES;
+        const int row = row_of(r);
         active[r] = row < N;
         base[r] = t.w[mi] + (size_t)(active[r] ? row : 0) * K + part * wsteps * 1024;
     }
@@ -429,7 +431,7 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
     }
     float sc[RW];
 #pragma unroll
-    for (int r = 0; r < RW; r++) sc[r] = t.scale[mi][active[r] ? row0 + r * GI_WAVES : 0];
+    for (int r = 0; r < RW; r++) sc[r] = t.scale[mi][active[r] ? row_of(r) : 0];
     __builtin_amdgcn_sched_barrier(0);  // x and the scales go out before the weights
     u4v v[RW][GW];
     u2v vt[RW];
@@ -459,6 +461,7 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
         }
     }
     __syncthreads();
+    float sum[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
         float acc = 0.f;
@@ -480,21 +483,28 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
                 for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[r][j], i), xv[i], acc);
             }
         }
-        float sum = wave_sum(acc);
-        if constexpr (S > 1) {
-            if (lane == 0) part_s[wave] = sum;
-            __syncthreads();
-            if (part != 0) return;
+        sum[r] = wave_sum(acc);
+    }
+    if constexpr (S > 1) {  // each row's parts meet in LDS and are added in part order by its first wave
 #pragma unroll
-            for (int p2 = 1; p2 < S; p2++) sum += part_s[wave + p2];
-        }
-        const int row = row0 + r * GI_WAVES;
+        for (int r = 0; r < RW; r++)
+            if (lane == 0) part_s[r * GI_WAVES + wave] = sum[r];
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int p2 = 1; p2 < S; p2++) sum[r] += part_s[r * GI_WAVES + wave + p2];
+    }
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int row = row_of(r);
         if (active[r] && lane == 0) {
-            sum *= sc[r];
+            float y = sum[r] * sc[r];
             const float* bias = t.bias[mi];
-            if (bias) sum = sum + bias[row];
-            if (XH) ((half_t*)t.out[mi])[row] = to_half(sum);
-            else ((float*)t.out[mi])[row] = sum;
+            if (bias) y = y + bias[row];
+            if (XH) ((half_t*)t.out[mi])[row] = to_half(y);
+            else ((float*)t.out[mi])[row] = y;
         }
     }
 }
@@ -507,7 +517,7 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_multi_kernel(const void* _
     constexpr int XS = ROT ? 1 : (4 * G + (TAIL ? 2 : 0) + GI_WAVES - 1) / GI_WAVES;
     constexpr int RS = (64 * G + (TAIL ? 32 : 0) + GI_WAVES * 64 - 1) / (GI_WAVES * 64) < 2 ? 1 : 2;
     extern __shared__ f4 xs[];
-    __shared__ float part_s[GI_WAVES];
+    __shared__ float part_s[4 * GI_WAVES];
     int mi = 0;
 #pragma unroll
     for (int i = 1; i < MULTI_MAX; i++)
@@ -515,10 +525,10 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_multi_kernel(const void* _
     const int blk = blockIdx.x - t.first[mi];
     switch (t.parts[mi]) {  // uniform over the workgroup
     case 4:
-        if constexpr (!TAIL && G >= 4) gemv_multi_rows<G / 4, 4, 1, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        if constexpr (!TAIL && G >= 4) gemv_multi_rows<G / 4, 4, 4, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
         break;
     case 2:
-        if constexpr (!TAIL && G >= 2) gemv_multi_rows<G / 2, 2, 1, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
+        if constexpr (!TAIL && G >= 2) gemv_multi_rows<G / 2, 2, 2, false, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
         break;
     default: gemv_multi_rows<G, 1, RW, TAIL, XH, ROT, XS, RS>(xin, t, mi, blk, K, group, rot_out, xs, part_s);
     }
@@ -920,7 +930,7 @@ int rda_gemv_i8_multi(const void* x, int x_half, int group, int count, const voi
         t.n[i] = n[i];
         t.parts[i] = gemv_parts(n[i], K);
         t.first[i] = (int)blocks;
-        const int rpb = t.parts[i] > 1 ? GI_WAVES / t.parts[i] : GI_WAVES * rw;
+        const int rpb = t.parts[i] > 1 ? GI_WAVES : GI_WAVES * rw;  // split rows: parts rows per wave
         blocks += (n[i] + rpb - 1) / rpb;
         if (blocks > 0x7fffffff) return RDA_ERR_INVALID;
     }
