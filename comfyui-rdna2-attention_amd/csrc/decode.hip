@@ -9,6 +9,10 @@
 #define SPLITS 32  // position chunks per (batch, kv head) in attn_decode
 #define HEAD 128
 
+// The sum of a value over the wave's 64 lanes, in every lane: DPP steps within each row of 16 lanes, then the lane
+// swaps across rows -- no LDS round trip (a butterfly of __shfl_xor is six ds_bpermute). Every GEMV, fused or not,
+// one matrix or several, reduces its lanes with this one order, so their outputs agree bit for bit.
+__device__ __forceinline__ float lane_total(float x) { return rows_sum(row_sum16(x)); }
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }
 
 // Position in the GEMVs' LDS copy of x of its f4 number i (values 4i .. 4i + 3), in reading order: the f4 j of lane
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_i8_kernel(const void* __restrict
             for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[j], i), xv[i], acc);
         }
     }
-    float sum = wave_sum(acc) * sc;
+    float sum = lane_total(acc) * sc;
     if (bias) sum = sum + bias[row];
     if (lane == 0) {
         if (XH) ((half_t*)out)[row] = to_half(sum);
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(GI_WAVES * 64) void gemv_i8_split_kernel(const void
 #pragma unroll
             for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(v[g][d], i), xf[d * 4 + i], acc);
     }
-    const float sum = wave_sum(acc);
+    const float sum = lane_total(acc);
     if (S > 1) {
         if (lane == 0) part_s[wave] = sum;
         __syncthreads();
@@ -483,7 +487,7 @@ __device__ __forceinline__ void gemv_multi_rows(const void* __restrict__ xin, co
                 for (int i = 0; i < 4; i++) acc = __builtin_fmaf(sbyte(vt[r][j], i), xv[i], acc);
             }
         }
-        sum[r] = wave_sum(acc);
+        sum[r] = lane_total(acc);
     }
     if constexpr (S > 1) {  // each row's parts meet in LDS and are added in part order by its first wave
 #pragma unroll
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(GV_WAVES * 64) void gemv_bf16_kernel(const float* _
     }
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        const float sum = wave_sum(acc[r]);
+        const float sum = lane_total(acc[r]);
         if (lane == 0) out[row + r] = sum;
     }
 }
