@@ -558,8 +558,7 @@ __global__ __launch_bounds__(256) void pack_k_i8_kernel(const half_t* __restrict
 #pragma unroll
         for (int i = 0; i < 8; i++) f[i] = 0.f;
     }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 16));
+    mx = row_max16(mx);  // over the key's 16 lanes
     const float scale = fmaxf(mx / 127.f, 1e-30f), rcp = 1.f / scale;
     u2v w;
 #pragma unroll

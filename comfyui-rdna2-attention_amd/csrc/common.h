@@ -109,19 +109,6 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float rcp) {
     return __builtin_fmaf(__builtin_fmaf(-y, s, x), rcp, y);
 }
 
-// Wave64 reductions. xor shuffles of width 64 stay exact for max; sums are
-// evaluated in the butterfly order (lane values paired at distance 32, 16, ...).
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 __device__ __forceinline__ i4v as_i4(u4v v) { return __builtin_bit_cast(i4v, v); }
 
 // Cross-lane reductions on DPP and lane-swap instructions (one VALU op per step, no LDS round trip).
@@ -143,6 +130,24 @@ __device__ __forceinline__ float row_max16(float x) {
     x = fmaxf(x, dpp<0x141>(x));
     x = fmaxf(x, dpp<0x140>(x));
     return x;
+}
+// The value of lane l ^ 4 and of lane l ^ 8, by two mirrors each (half-row i <-> 7 - i, quad i <-> 3 - i, row
+// i <-> 15 - i): exact partners, no LDS round trip.
+__device__ __forceinline__ float lane_xor4(float x) { return dpp<0x1B>(dpp<0x141>(x)); }
+__device__ __forceinline__ float lane_xor8(float x) { return dpp<0x141>(dpp<0x140>(x)); }
+// sum += __shfl_xor(sum, o) for o = W / 2, ..., 2, 1 (W = 32 or 16), with the same partners, so the same bits (each
+// step adds the same two values in every lane of a pair; IEEE addition is commutative).
+template <int W>
+__device__ __forceinline__ float xor_butterfly_sum(float x) {
+    static_assert(W == 32 || W == 16, "32- or 16-lane butterflies");
+    if constexpr (W == 32) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        x = __uint_as_float(a[0]) + __uint_as_float(a[1]);  // lanes l and l ^ 16
+    }
+    x += lane_xor8(x);
+    x += lane_xor4(x);
+    x += dpp<0x4E>(x);
+    return x + dpp<0xB1>(x);
 }
 // Over the four rows (lanes l, l ^ 16, l ^ 32, l ^ 48).
 __device__ __forceinline__ float rows_sum(float x) {

@@ -10,7 +10,7 @@
 #define HEAD 128
 
 // The sum of a value over the wave's 64 lanes, in every lane: DPP steps within each row of 16 lanes, then the lane
-// swaps across rows -- no LDS round trip (a butterfly of __shfl_xor is six ds_bpermute). Every GEMV, fused or not,
+// swaps across rows -- no LDS round trip (a butterfly of shuffles would be six ds_bpermute). Every GEMV, fused or not,
 // one matrix or several, reduces its lanes with this one order, so their outputs agree bit for bit.
 __device__ __forceinline__ float lane_total(float x) { return rows_sum(row_sum16(x)); }
 __device__ __forceinline__ float sbyte(u32 w, int i) { return (float)((int)(w << (24 - 8 * i)) >> 24); }

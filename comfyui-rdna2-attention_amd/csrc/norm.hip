@@ -46,8 +46,7 @@ __global__ __launch_bounds__(NT) void norm_kernel(const half_t* __restrict__ X, 
             for (int j = 0; j < 8; j++) sum = __builtin_fmaf((float)v[c][j], (float)v[c][j], sum);
         }
     }
-#pragma unroll
-    for (int o = (TPR < 32 ? TPR : 32) / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+    sum = xor_butterfly_sum<(TPR < 32 ? TPR : 32)>(sum);
     if (TPR > 32) {
         if ((threadIdx.x & 31) == 0) red[threadIdx.x >> 5] = sum;
         __syncthreads();

@@ -149,8 +149,7 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                     for (int j = 0; j < 8; j++) sum = __builtin_fmaf((float)v[j], (float)v[j], sum);
                 }
             }
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+            sum = xor_butterfly_sum<32>(sum);
             static_assert(ACT != MOD || NW * 64 == QT, "the MOD sum of squares needs the reference's 256 threads");
             if ((t & 31) == 0) red[t >> 5] = sum;
             __syncthreads();
@@ -277,7 +276,7 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
             wave_sync();
         }
     }
-    mx = wave_max(mx);
+    mx = rows_max(row_max16(mx));  // the wave's maximum (exact in any order)
     __syncthreads();
     if (lane == 0) red[wave] = mx;
     __syncthreads();
