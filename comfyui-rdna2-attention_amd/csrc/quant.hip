@@ -113,11 +113,21 @@ __device__ __forceinline__ u32 pack4(int a, int b, int c, int d) {
 // launcher sizes it to the row (K / 1024 waves, so that K = 3072 keeps every lane busy in both passes: the kernel
 // is vector-ALU bound); MOD keeps 4 (QT threads), whose sum of squares follows the reference's thread order.
 // IL: the codes k-interleaved (each 8 values of k stored as their 4 even ones, then their 4 odd ones).
+// WL (the rotations other than MOD): each wave keeps the rotated fp16 values of its own passes (1024 values each) in an
+// LDS region of its own -- pass p at SW_BYTES + 2048 p, the last pass inside its transpose buffer, free by then -- and
+// quantizes them itself once the row maximum is known, so a row takes NW (SW_BYTES + 2048 (passes - 1)) bytes of LDS
+// instead of 2 K + NW SW_BYTES (K = 3072: 13.1 against 19.2 KiB; more rows in flight per CU). MOD stages its input
+// row in LDS for the sum of squares and rotates in place there.
+#define SW_BYTES (64 * 17 * 4)  // a wave's transpose buffer: 17 floats per lane
+template <int GROUP, int NW>
+__host__ __device__ constexpr int rot_passes(int K) { return (K / GROUP + NW * (1024 / GROUP) - 1) / (NW * (1024 / GROUP)); }
+
 template <int ACT, bool I4, int GROUP, int NW, bool IL>
 __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __restrict__ X, long ldx, const half_t* __restrict__ U,
                                                        int8_t* __restrict__ Aq, float* __restrict__ as, int K, ModArgs mod) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     __shared__ float red[8];
+    constexpr bool WL = GROUP != 0 && ACT != MOD;
     half_t* rotated = (half_t*)smem;
     const int row = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const half_t* x = X + (size_t)row * ldx;
@@ -162,7 +172,9 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
         constexpr int LPG = GROUP / 16;  // lanes per group, 16 values each
         constexpr int GPW = 64 / LPG;    // groups per wave per pass
         const int gl = lane / LPG, c = lane % LPG, groups = K / GROUP;
-        float* sw = (float*)(smem + (size_t)K * 2) + (wave * 64 + gl * LPG) * 17;
+        const int passes = rot_passes<GROUP, NW>(K), wreg = SW_BYTES + 2048 * (passes - 1);  // WL: a wave's LDS region
+        char* wbase = WL ? smem + (size_t)wave * wreg : smem + (size_t)K * 2 + (size_t)wave * SW_BYTES;
+        float* sw = (float*)wbase + gl * LPG * 17;
         const size_t mrow = ACT == MOD ? (size_t)(row / mod.L) * K : 0;
         const half_t* ms = ACT == MOD ? mod.s + mrow : nullptr;
         const half_t* mt = ACT == MOD ? mod.t + mrow : nullptr;
@@ -234,14 +246,10 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
             }
             wave_sync();
             if (active) {
-                int e[16];
                 if (GROUP == 256) {
                     // Lane c now holds elements c + 16i: digits at strides 16 and 64.
 #pragma unroll
-                    for (int i = 0; i < 16; i++) {
-                        v[i] = sw[i * 17 + c];
-                        e[i] = i * 16 + c;
-                    }
+                    for (int i = 0; i < 16; i++) v[i] = sw[i * 17 + c];
                     h16(v);
                 } else {
                     // Lane c takes the columns c and c + 8 (elements c + 16i, c + 8 + 16i, i < 8):
@@ -250,8 +258,6 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                     for (int i = 0; i < 8; i++) {
                         v[i] = sw[i * 17 + c];
                         v[8 + i] = sw[i * 17 + c + 8];
-                        e[i] = c + 16 * i;
-                        e[8 + i] = c + 8 + 16 * i;
                     }
 #pragma unroll
                     for (int b = 0; b < 16; b += 4) h4(v[b], v[b + 1], v[b + 2], v[b + 3]);
@@ -264,12 +270,18 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
                             v[b + i + 4] = p - q;
                         }
                 }
-                // The row maximum is taken before the rounding to fp16 and rounded once at the end: rounding is monotonic,
-                // so max(round |p|) = round(max |p|), one conversion per element fewer.
+            }
+            // The row maximum is taken before the rounding to fp16 and rounded once at the end: rounding is monotonic,
+            // so max(round |p|) = round(max |p|), one conversion per element fewer.
+            const int p = (g0 - wave * GPW) / (NW * GPW);
+            if (WL && p == passes - 1) wave_sync();  // the last pass reuses the transpose buffer: every lane has read it
+            if (active) {
+                half_t* dst = WL ? (half_t*)(wbase + (p == passes - 1 ? 0 : SW_BYTES + 2048 * p)) + gl * GROUP : rotated + g * GROUP;
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
                     const float y = v[i] * norm;
-                    rotated[g * GROUP + e[i]] = to_half(y);
+                    // element of the group: c + 16 i (GROUP 256); c + 16 i and c + 8 + 16 (i - 8) (GROUP 128)
+                    dst[GROUP == 256 ? c + 16 * i : c + (i < 8 ? 16 * i : 8 + 16 * (i - 8))] = to_half(y);
                     mx = fmaxf(mx, fabsf(y));
                 }
             }
@@ -289,9 +301,8 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
 
     const float rcp = 1.f / scale;
     int8_t* out = Aq + (size_t)row * K;
-    const h8* src = staged ? (const h8*)rotated : (const h8*)x;
-    for (int ch = t; ch < K / 16; ch += NW * 64) {
-        const h8 lo = src[ch * 2], hi = src[ch * 2 + 1];
+    // The 16 codes of the row's chunk ch (values 16 ch ..) from its fp16 values lo, hi, stored in one 16-byte write.
+    auto quant16 = [&](const h8 lo, const h8 hi, int ch) __attribute__((always_inline)) {
         const u4v wl = __builtin_bit_cast(u4v, lo), wh = __builtin_bit_cast(u4v, hi);
         int q[16];
 #pragma unroll
@@ -322,12 +333,27 @@ __global__ __launch_bounds__(NW * 64) void rot_quant_kernel(const half_t* __rest
             for (int d = 0; d < 4; d++) o[d] = pack4(q[d * 4], q[d * 4 + 1], q[d * 4 + 2], q[d * 4 + 3]);
         }
         *(u4v*)(out + ch * 16) = o;
+    };
+    if constexpr (WL) {
+        // Each wave its own passes: lane l takes values 16 l .. of pass p's 1024 (chunk (wave + NW p) 64 + l of the row).
+        const int passes = rot_passes<GROUP, NW>(K), wreg = SW_BYTES + 2048 * (passes - 1);
+        for (int p = 0; p < passes; p++) {
+            const int ch = (wave + NW * p) * 64 + lane;
+            if (ch >= K / 16) break;  // past the row's groups (a wave's later passes may hold none)
+            const h8* from = (const h8*)(smem + (size_t)wave * wreg + (p == passes - 1 ? 0 : SW_BYTES + 2048 * p)) + lane * 2;
+            quant16(from[0], from[1], ch);
+        }
+    } else {
+        const h8* src = staged ? (const h8*)rotated : (const h8*)x;
+        for (int ch = t; ch < K / 16; ch += NW * 64) quant16(src[ch * 2], src[ch * 2 + 1], ch);
     }
 }
 
 template <int ACT, bool I4, int GROUP, int NW>
 static int launch_rot_quant_nw(const void* x, long ldx, const void* u, void* aq, float* as, int M, int K, ModArgs mod, void* stream, int il) {
-    const size_t lds = GROUP ? (size_t)K * 2 + NW * 64 * 17 * sizeof(float) : K <= MAX_LDS_K ? (size_t)K * 2 : 0;
+    const size_t lds = GROUP == 0 ? (K <= MAX_LDS_K ? (size_t)K * 2 : 0)
+                       : ACT == MOD ? (size_t)K * 2 + NW * SW_BYTES
+                                    : (size_t)NW * (SW_BYTES + 2048 * (rot_passes<GROUP ? GROUP : 16, NW>(K) - 1));
     if (il) {  // k-interleaved codes: the plain rotation only
         if constexpr (ACT == NO_ACT && !I4 && GROUP != 0)
             hipLaunchKernelGGL((rot_quant_kernel<ACT, I4, GROUP, NW, true>), dim3(M), dim3(NW * 64), lds, (hipStream_t)stream, (const half_t*)x, ldx,
