@@ -28,9 +28,12 @@
 // base + 16 i), issued one step ahead, so no register holds a tile in flight and the load
 // latency hides behind a full step of work; the s_waitcnt before each step's closing barrier is
 // where the copies are awaited. The loop is software-pipelined: step i computes the scores of
-// tile i + 1 while tile i's exponentials run between those products (the transcendental unit
-// works beside the matrix cores; plain VALU work does not), then tile i's PV product -- so
-// tiles i and i + 1 are read while tile i + 2 arrives. Both tiles are row-major, 256 bytes per key
+// tile i + 1 with exponentials of tile i between those products, then tile i's PV product with
+// exponentials of tile i + 1 between its products (fp16: half of a tile's exponentials in each
+// phase; int8: all beside the score products) -- so tiles i and i + 1 are read while tile i + 2
+// arrives. Vector work issues beside the matrix products of the same SIMD, but not for free: a
+// phase with a 6-instruction part beside every product slows its products down (the step
+// schedule below). Both tiles are row-major, 256 bytes per key
 // (int8 K: 128), with the 16-byte chunks of a row permuted by an XOR swizzle so that the
 // reads below hit distinct banks: K chunk c of key r sits at c ^ (r & 15) (int8: c ^ (r & 7)),
 // V chunk c at c ^ 4 (r & 3).
@@ -380,16 +383,32 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     float s[16];
     h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
     constexpr int PARTS = I8 ? 4 : 8, PER = 16 / PARTS;
-    auto exps = [&](int k) __attribute__((always_inline)) {
+    auto exps_of = [&](const float (&x)[16], int k) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = k * PER; r < (k + 1) * PER; r += 2) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], I8 ? score_scale : p.scale_log2, -m));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r + 1], I8 ? score_scale : p.scale_log2, -m));
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], I8 ? score_scale : p.scale_log2, -m));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r + 1], I8 ? score_scale : p.scale_log2, -m));
             const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
             l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);  // l sums the fp16 P of PV
             pf[r >> 3][r & 7] = pk[0];
             pf[r >> 3][(r & 7) + 1] = pk[1];
         }
+    };
+    auto exps = [&](int k) __attribute__((always_inline)) { exps_of(s, k); };
+    // fp16: part k (< 4: keys 0-15) of the next tile's P into registers of its own, pinned where it is issued (the
+    // empty asm consumes the results: without it the parts placed beside the PV products sink past the step's
+    // closing barrier to their first use).
+    auto exps_to = [&](const float (&x)[16], int k, h8& d) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = k * PER; r < (k + 1) * PER; r += 2) {
+            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], p.scale_log2, -m));
+            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r + 1], p.scale_log2, -m));
+            const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
+            l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);
+            d[r & 7] = pk[0];
+            d[(r & 7) + 1] = pk[1];
+        }
+        asm volatile("" : "+v"(d), "+v"(l));
     };
     // The lazy rescale (hip_attention.hip:333-340): m moves only when some row's tile maximum exceeds m + 8. The tile's P
     // is first made with the current m; a row whose maximum exceeds m + 8 has a P of at least ~2^7.8 in one of its two
@@ -423,7 +442,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     };
     // O^T += V^T P^T with the V tile of stage `stage` and P in pf. Each V^T operand of the second 16-key step is read
     // into the registers the matching first-step product has just consumed.
-    auto pv = [&](auto stage, auto&& hook) __attribute__((always_inline)) {
+    auto pv = [&](auto stage, auto&& hook, auto&& hook2) __attribute__((always_inline)) {
         const u32 st_u = (u32)((int)stage * VS);
         u32 vb = v_base;
         asm volatile("" : "+v"(vb));
@@ -443,13 +462,18 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], pf[1], o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 4; dt++) {
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[dt], pf[1], o[dt], 0, 0, 0);
+            hook2(dt);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // Tile loop, software-pipelined over three LDS stages. At the start of step i, tiles i and i + 1 are in LDS and
-    // s holds tile i's scores. Step i issues the copies of tile i + 2 (into the stage tile i - 1 left), computes
-    // tile i + 1's scores with tile i's exponentials between the products, settles the rescale, runs tile i's PV
-    // product, and awaits tile i + 2 at the barrier closing the step (which also retires every read of tile i's
+    // s holds tile i's scores (fp16: and tile i's P for keys 0-15). Step i issues the copies of tile i + 2 (into the
+    // stage tile i - 1 left), computes tile i + 1's scores with tile i's (remaining) exponentials between the
+    // products, settles the rescale, runs tile i's PV product (fp16: with tile i + 1's first exponentials between its
+    // products), and awaits tile i + 2 at the barrier closing the step (which also retires every read of tile i's
     // stage before step i + 1 copies into it). Tile t sits in stage (t - tiles + 1) mod 3, so the last tile is in
     // stage 0 and the one before it in stage 2. The steady steps run six to a loop pass -- stages 2, 0, 1 twice,
     // which also returns the scores to the registers they started in (they alternate between two sets) -- after
@@ -461,32 +485,43 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     using Steady = std::integral_constant<int, 0>;
     using Penult = std::integral_constant<int, 1>;
     using Last = std::integral_constant<int, 2>;
+    // fp16: a tile's exponentials run in two halves, keys 0-15 beside the previous tile's PV products (into registers
+    // of their own, since those products still read the previous tile's P) and keys 16-31 beside the next tile's
+    // score products, one part of four exponential pairs beside every other product in each phase. With all of them
+    // beside the score products (the int8 layout), that phase was vector-ALU bound while the PV phase had almost no
+    // vector work: 194.7 -> 188.1 us at B=1, H=24, S=4096, bit-identical, in one process (keys 0-15 beside only the
+    // last four PV products, which do not read them, so no second P buffer: 190.1 us). l_old (l before the tile's
+    // first half) then carries over from the step before.
+    float l_old = 0.f;
     auto step = [&](int i, auto stage, auto kind) __attribute__((always_inline)) {
         constexpr int K = decltype(kind)::value;
         const auto next = next_stage(stage);
         if constexpr (K == 0) issue((i + 2) * KB, (int)next_stage(next));
-        const float l_old = l;
+        if constexpr (I8) l_old = l;
         if constexpr (K != 2) {
             float nxt[16];
             if constexpr (I8) {
                 i16v raw;
                 qk_raw(next, raw, exps);
                 settle(stage, i * KB, std::false_type{}, l_old);
-                pv(stage, [&](int dt) { scale_part(next, raw, nxt, dt); });
+                pv(stage, [&](int dt) { scale_part(next, raw, nxt, dt); }, no_hook);
                 if constexpr (K == 1) mask(nxt, (i + 1) * KB);
             } else {
-                qk(next, nxt, exps);
+                qk(next, nxt, [&](int k) { if (k & 1) exps(4 + (k >> 1)); });
                 if constexpr (K == 1) mask(nxt, (i + 1) * KB);
                 settle(stage, i * KB, std::false_type{}, l_old);
-                pv(stage, no_hook);
+                l_old = l;
+                h8 pn;
+                pv(stage, [&](int dt) { if (dt & 1) exps_to(nxt, dt >> 1, pn); }, [&](int dt) { if (dt & 1) exps_to(nxt, 2 + (dt >> 1), pn); });
+                pf[0] = pn;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) s[r] = nxt[r];
         } else {
 #pragma unroll
-            for (int k = 0; k < PARTS; k++) exps(k);
+            for (int k = I8 ? 0 : PARTS / 2; k < PARTS; k++) exps(k);
             settle(stage, i * KB, std::true_type{}, l_old);
-            pv(stage, no_hook);
+            pv(stage, no_hook, no_hook);
         }
         if constexpr (K == 0) {
             wait_copies();
@@ -501,9 +536,15 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     if (tiles == 1) {
         qk(S0{}, s, no_hook);
         mask(s, 0);
+        if constexpr (!I8)
+#pragma unroll
+            for (int k = 0; k < PARTS / 2; k++) exps(k);
         step(0, S0{}, Last{});
     } else {
         qk(first, s, no_hook);
+        if constexpr (!I8)
+#pragma unroll
+            for (int k = 0; k < PARTS / 2; k++) exps(k);
         const int steady = tiles - 2, peel = steady % 6;
         if (peel >= 5) step(peel - 5, S0{}, Steady{});
         if (peel >= 4) step(peel - 4, S1{}, Steady{});
