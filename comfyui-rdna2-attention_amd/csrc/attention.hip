@@ -383,31 +383,25 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(3, 3))
     float s[16];
     h8 pf[2];  // P, packed for the two 16-key steps: step j holds registers 8 j .. 8 j + 7
     constexpr int PARTS = I8 ? 4 : 8, PER = 16 / PARTS;
-    auto exps_of = [&](const float (&x)[16], int k) __attribute__((always_inline)) {
+    // Part k of the P of scores x into d0 (keys 0-15) and d1 (keys 16-31).
+    auto exps_into = [&](const float (&x)[16], int k, h8& d0, h8& d1) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = k * PER; r < (k + 1) * PER; r += 2) {
             const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], I8 ? score_scale : p.scale_log2, -m));
             const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r + 1], I8 ? score_scale : p.scale_log2, -m));
             const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
             l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);  // l sums the fp16 P of PV
-            pf[r >> 3][r & 7] = pk[0];
-            pf[r >> 3][(r & 7) + 1] = pk[1];
+            h8& d = r < 8 ? d0 : d1;
+            d[r & 7] = pk[0];
+            d[(r & 7) + 1] = pk[1];
         }
     };
-    auto exps = [&](int k) __attribute__((always_inline)) { exps_of(s, k); };
+    auto exps = [&](int k) __attribute__((always_inline)) { exps_into(s, k, pf[0], pf[1]); };
     // fp16: part k (< 4: keys 0-15) of the next tile's P into registers of its own, pinned where it is issued (the
     // empty asm consumes the results: without it the parts placed beside the PV products sink past the step's
     // closing barrier to their first use).
     auto exps_to = [&](const float (&x)[16], int k, h8& d) __attribute__((always_inline)) {
-#pragma unroll
-        for (int r = k * PER; r < (k + 1) * PER; r += 2) {
-            const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r], p.scale_log2, -m));
-            const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x[r + 1], p.scale_log2, -m));
-            const h2 pk = __builtin_convertvector((f2){e0, e1}, h2);
-            l = __builtin_amdgcn_fdot2(pk, (h2){(_Float16)1.f, (_Float16)1.f}, l, false);
-            d[r & 7] = pk[0];
-            d[(r & 7) + 1] = pk[1];
-        }
+        exps_into(x, k, d, d);
         asm volatile("" : "+v"(d), "+v"(l));
     };
     // The lazy rescale (hip_attention.hip:333-340): m moves only when some row's tile maximum exceeds m + 8. The tile's P
