@@ -21,8 +21,10 @@ faster is the baseline's value.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-components] [--no-cpu] [--only NAME] [--cpu-only]
 
-"decode_layer" times one token through one Qwen3-8B-shaped layer's int8 linears and decode attention, and
-"dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192, 4096 tokens).
+"attention_f16_s1024" times the fp16 attention at 1024 tokens (the DiT at 512 x 512), where the workgroup layout
+differs from the headline's; "decode_layer" times one token through one Qwen3-8B-shaped layer's int8 linears and
+decode attention; "dit_block" times the whole fused Krea 2 block (int8_gemm.block_forward at hidden 3072, MLP 8192,
+4096 tokens).
 
 `--only NAME` runs one workload (the names of "components", "attention_f16", "copy": a 1 GiB device copy used to
 calibrate FETCH_SIZE / WRITE_SIZE, or "mfma_peak_i8" / "mfma_peak_f16": back-to-back MFMAs, the sustained matrix rate)
@@ -148,12 +150,16 @@ def roofline(bound, achieved, peak, unit, traffic=None):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
-def attention_inputs(torch):
-    shape = (1, 24, 4096, 128)
+def attention_inputs(torch, S=4096):
+    shape = (1, 24, S, 128)
     return tuple(torch.randn(*shape, generator=gen(torch, s)).half() for s in (4, 5, 6))
 
 
-ATTN_FLOP = 4.0 * 24 * 4096 ** 2 * 128
+def attn_flop(S):
+    return 4.0 * 24 * S ** 2 * 128
+
+
+ATTN_FLOP = attn_flop(4096)
 
 
 def load_traffic():
@@ -172,6 +178,15 @@ def w_attention(torch, dev, int8_qk=False):
     q, k, v = (t.to(dev) for t in attention_inputs(torch))
     out = torch.empty_like(q)
     return (lambda i: hip_attention.attention(q, k, v, out, 128 ** -0.5, int8_qk)), 1, ATTN_FLOP, "mfma_f16", event_timed
+
+
+def w_attention_s1024(torch, dev):
+    """The fp16 attention at 1024 tokens (B=1, H=24, D=128: the DiT at 512 x 512), where 24 x 1024 query rows fill a
+    quarter of the CUs with twelve-wave workgroups and the four-wave layout is chosen. ~25 us: graph-replayed."""
+    from comfyui_rdna2_attention_amd import hip_attention
+    q, k, v = (t.to(dev) for t in attention_inputs(torch, 1024))
+    out = torch.empty_like(q)
+    return (lambda i: hip_attention.attention(q, k, v, out, 128 ** -0.5)), 1, attn_flop(1024), "mfma_f16", graph_timed
 
 
 def _w8a8_inputs(torch, dev):
@@ -446,6 +461,7 @@ def w_copy(torch, dev):
 WORKLOADS = {
     "attention_f16": lambda t, d: w_attention(t, d, False),
     "attention_i8qk": lambda t, d: w_attention(t, d, True),
+    "attention_f16_s1024": w_attention_s1024,
     "w8a8_gemm": w_w8a8_gemm,
     "w8a8_rot_quant": w_w8a8_rot_quant,
     "w8a8_linear": w_w8a8_linear,
@@ -469,7 +485,7 @@ WORKLOADS = {
 NOT_COMPONENTS = ("attention_f16", "copy", "mfma_peak_i8", "mfma_peak_f16", "mfma_peak_i8_random", "mfma_peak_f16_random")
 PEAKS = {"mfma_f16": ("mfma", PEAK_F16_TFLOPS, "TFLOP/s"), "mfma_i8": ("mfma", PEAK_I8_TOPS, "TFLOP/s"), "hbm": ("hbm", PEAK_HBM_GBS, "GB/s")}
 # The roofline of each workload (the 4th item its function returns), for the CPU leg, which runs without a GPU.
-WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
+WORKLOAD_BOUND = {"attention_f16": "mfma_f16", "attention_i8qk": "mfma_f16", "attention_f16_s1024": "mfma_f16", "w8a8_gemm": "mfma_i8", "w8a8_rot_quant": "hbm", "w8a8_linear": "mfma_i8",
                   "w4a8_gemm": "mfma_i8", "w4a8_gemm_k12288": "mfma_i8", "mlp_rms_norm": "hbm", "mlp_swiglu_rot_quant": "hbm", "mlp_down_gemm": "mfma_i8", "decode_gemv_n4096": "hbm",
                   "decode_gemv_n1024": "hbm", "decode_gemv_n12288": "hbm", "decode_attention": "hbm", "decode_layer": "hbm", "dit_block": "mfma_i8",
                   "copy": "hbm", "mfma_peak_i8": "mfma_i8", "mfma_peak_f16": "mfma_f16", "mfma_peak_i8_random": "mfma_i8",
@@ -503,12 +519,12 @@ def _cpu_w8a8(torch):
     return M, K, N, x, w, ws
 
 
-def c_attention(torch, heads=2, dtype=None):
+def c_attention(torch, heads=2, dtype=None, S=4096):
     from oracle import cpu_baseline as cb
     dt = dtype or torch.float32
-    q, k, v = (t[:, :heads].to(dt).contiguous() for t in attention_inputs(torch))
-    return (lambda: cb.attention_bmm(q, k, v, 128 ** -0.5)), ATTN_FLOP * heads / 24, \
-        f"attention_bmm (attention.py:15-43) in {dt_name(dt)} over {heads} of the 24 heads, S=4096, D=128"
+    q, k, v = (t[:, :heads].to(dt).contiguous() for t in attention_inputs(torch, S))
+    return (lambda: cb.attention_bmm(q, k, v, 128 ** -0.5)), attn_flop(S) * heads / 24, \
+        f"attention_bmm (attention.py:15-43) in {dt_name(dt)} over {heads} of the 24 heads, S={S}, D=128"
 
 
 def c_w8a8_gemm(torch, dtype=None):
@@ -649,6 +665,7 @@ def c_dit_block(torch, L=1024):
 CPU_BASELINES = {
     "attention_f16": c_attention,
     "attention_i8qk": c_attention,
+    "attention_f16_s1024": lambda t, **kw: c_attention(t, S=1024, **kw),
     "w8a8_gemm": c_w8a8_gemm,
     "w8a8_rot_quant": c_w8a8_rot_quant,
     "w8a8_linear": c_w8a8_linear,
@@ -669,7 +686,7 @@ CPU_BASELINES = {
 # Workloads whose reference fallback also runs in the activations' dtype (fp16): timed in fp32 and fp16, and the
 # faster is the baseline (both are reported). The others are fp32 by construction (the fp32 cast RMSNorm, the fp32
 # ConvRot before quantization, the fp32 decode cache, the unfused block in fp32).
-F16_BASELINES = ("attention_f16", "attention_i8qk", "w8a8_gemm", "w8a8_linear", "w4a8_gemm", "w4a8_gemm_k12288", "mlp_down_gemm",
+F16_BASELINES = ("attention_f16", "attention_i8qk", "attention_f16_s1024", "w8a8_gemm", "w8a8_linear", "w4a8_gemm", "w4a8_gemm_k12288", "mlp_down_gemm",
                  "decode_gemv_n4096", "decode_gemv_n1024", "decode_gemv_n12288")
 
 

@@ -36,6 +36,8 @@ SIGNATURES = {
     "rda_attn_i8_workspace": (_sz, [_i, _i, _i]),
     "rda_pack_k_i8": (_i, [_p, _p, _i, _i, _i, _l, _l, _l, _p]),
     "rda_attn_i8": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _f, _p]),
+    "rda_attn_waves": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _f, _i, _p]),
+    "rda_attn_i8_waves": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _f, _i, _p]),
     "rda_rotate": (_i, [_p, _p, _i, _i, _p]),
     "rda_gemv_i8": (_i, [_p, _i, _p, _p, _p, _p, _i, _i, _p]),
     "rda_rotate_gemv_i8": (_i, [_p, _i, _p, _p, _p, _p, _p, _i, _i, _p]),

@@ -641,15 +641,42 @@ static int launch_attn_waves(const AttnArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-// Twelve-wave workgroups when every head has at least 384 query rows (a workgroup's rows, each head's padded to a
-// multiple of 32, then span at most two heads); four-wave ones otherwise.
+// The current device's compute units, read once per device.
+static int device_cus(int* cus) {
+    static std::atomic<int> known[RDA_MAX_DEVICES];
+    int dev = 0;
+    if (const hipError_t e = hipGetDevice(&dev)) return (int)e;
+    if (dev < 0 || dev >= RDA_MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    int n = known[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (const hipError_t e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev)) return (int)e;
+        known[dev].store(n, std::memory_order_relaxed);
+    }
+    *cus = n;
+    return 0;
+}
+
+// Workgroup layout: twelve waves over 384 rows of the (batch, head, row) range (every head of at least 384 query rows,
+// so that a workgroup's rows span at most two heads), or four waves over 128 rows of one head. The twelve-wave grid
+// has a third as many workgroups, one per CU: it is the faster one only when it still covers most of the chip. B = 1,
+// H = 24, fp16, one process: 1024 rows per head (64 twelve-wave workgroups) 45.2 us twelve-wave against 24.6 us
+// four-wave, 2048 (128) 77.7 / 62.4, 2560 (160) 96.0 / 84.5, 2816 (176) 108.6 / 120.1, 3072 (192) 121.1 / 134.7,
+// 4096 (256) 193.0 / 199.6; int8-QK alike, and the outputs bit-identical. So twelve waves when their grid covers at
+// least two thirds of the CUs. waves: 0 chooses so; 4 or 12 fixes the layout (12 needs Lq >= 384).
 template <bool I8>
-static int launch_attn(AttnArgs a, void* stream) {
-    if (a.Lq >= FLAT_ROWS) {
-        a.nblocks = (int)((a.rows + FLAT_ROWS - 1) / FLAT_ROWS);
+static int launch_attn(AttnArgs a, int waves, void* stream) {
+    const long flat = (a.rows + FLAT_ROWS - 1) / FLAT_ROWS;
+    if (waves == 0) {
+        int cus = 0;
+        if (const int e = device_cus(&cus)) return e;
+        waves = a.Lq >= FLAT_ROWS && 3 * flat >= 2L * cus ? 12 : 4;
+    }
+    if (waves == 12 && a.Lq >= FLAT_ROWS && flat < (1L << 31)) {
+        a.nblocks = (int)flat;
         return launch_attn_waves<I8, 12>(a, stream);
     }
-    return launch_attn_waves<I8, 4>(a, stream);
+    if (waves == 4) return launch_attn_waves<I8, 4>(a, stream);
+    return RDA_ERR_INVALID;
 }
 
 // Row strides of K and V must keep a tile's 32 rows within 2^31 bytes (the kernel's 32-bit per-lane offsets).
@@ -669,11 +696,16 @@ size_t rda_attn_i8_workspace(int B, int Hkv, int Lk) {
     return (size_t)B * Hkv * pad * 128 + (size_t)B * Hkv * pad * 4;
 }
 
-int rda_attn(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
-             void* stream) {
+int rda_attn_waves(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
+                   int waves, void* stream) {
     if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
     if (!dma_ready(k, strides[3], strides[4], strides[5]) || !dma_ready(v, strides[6], strides[7], strides[8])) return RDA_ERR_INVALID;
-    return launch_attn<false>(make_args(q, k, v, out, B, H, Hkv, Lq, Lk, strides, scale), stream);
+    return launch_attn<false>(make_args(q, k, v, out, B, H, Hkv, Lq, Lk, strides, scale), waves, stream);
+}
+
+int rda_attn(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
+             void* stream) {
+    return rda_attn_waves(q, k, v, out, B, H, Hkv, Lq, Lk, strides, scale, 0, stream);
 }
 
 int rda_pack_k_i8(const void* k, void* workspace, int B, int Hkv, int Lk, long skb, long skh, long skl, void* stream) {
@@ -686,14 +718,19 @@ int rda_pack_k_i8(const void* k, void* workspace, int B, int Hkv, int Lk, long s
     return (int)hipGetLastError();
 }
 
-int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
-                float scale, void* stream) {
+int rda_attn_i8_waves(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
+                      float scale, int waves, void* stream) {
     if (!attn_shapes_ok(B, H, Hkv, Lq, Lk, strides)) return RDA_ERR_INVALID;
     if (((uintptr_t)workspace & 15) != 0 || !dma_ready(v, strides[6], strides[7], strides[8])) return RDA_ERR_INVALID;
     AttnArgs a = make_args(q, nullptr, v, out, B, H, Hkv, Lq, Lk, strides, scale);
     a.k8 = (const int8_t*)workspace;
     a.ks = (const float*)(a.k8 + (size_t)B * Hkv * a.Lk_pad * 128);
-    return launch_attn<true>(a, stream);
+    return launch_attn<true>(a, waves, stream);
+}
+
+int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
+                float scale, void* stream) {
+    return rda_attn_i8_waves(q, workspace, v, out, B, H, Hkv, Lq, Lk, strides, scale, 0, stream);
 }
 
 }  // extern "C"

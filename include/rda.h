@@ -112,6 +112,15 @@ int rda_pack_k_i8(const void* k, void* workspace, int B, int Hkv, int Lk, long s
 int rda_attn_i8(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
                 void* stream);
 
+/* rda_attn / rda_attn_i8 with the workgroup layout fixed: waves 4 (four-wave workgroups of 128 rows of one head) or 12
+ * (twelve-wave workgroups of 384 rows of the (batch, head, row) range; needs Lq >= 384), or 0 for the choice
+ * rda_attn makes (twelve waves when Lq >= 384 and their grid covers at least two thirds of the CUs). Both layouts
+ * give the same bits. No reference counterpart: for tests and measurement of each layout. Other values return 1. */
+int rda_attn_waves(const void* q, const void* k, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides, float scale,
+                   int waves, void* stream);
+int rda_attn_i8_waves(const void* q, const void* workspace, const void* v, void* out, int B, int H, int Hkv, int Lq, int Lk, const long* strides,
+                      float scale, int waves, void* stream);
+
 /* ------------------------------------------------------------------ decode path ---------- */
 
 /* rotate, int8_gemv.py:42-45 (int8_gemv.hip:31-52): fp32 rows of `group` (a power of 4). */

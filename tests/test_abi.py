@@ -85,8 +85,8 @@ def test_library_loads_and_binds(built):
 
 def test_argument_checks_reject_before_any_launch(built):
     """Checks that return RDA_ERR_INVALID before the device is touched (the pointers are never dereferenced): the
-    fused rotation's output overlapping its input, rows or outputs not on 16-byte boundaries, and the multi-matrix
-    GEMV's table limits."""
+    fused rotation's output overlapping its input, rows or outputs not on 16-byte boundaries, the multi-matrix
+    GEMV's table limits, and attention layouts that do not exist or do not fit the rows."""
     lib = _lib.declare(ctypes.CDLL(built))
     a = 1 << 20  # a 16-byte aligned address, never read
     K = 4096
@@ -106,6 +106,10 @@ def test_argument_checks_reject_before_any_launch(built):
     assert lib.rda_gemv_i8_multi(a, 0, 256, 2, ptrs, ptrs, None, ptrs, n, 12288, None, None) == 1  # K past 8192
     assert lib.rda_gemv_i8_multi(a, 1, 256, 2, ptrs, ptrs, None, ptrs, n, K, None, None) == 1  # fp16 x with a rotation
     assert lib.rda_gemv_i8_multi(a, 0, 256, 2, ptrs, ptrs, None, ptrs, n, K, a + 16, None) == 1  # rotation onto x
+    strides = _lib.long_array([384 * 128, 384 * 128, 128] * 4)
+    for waves, lq in ((5, 384), (8, 384), (12, 383), (12, 32)):  # no such layout; twelve waves need 384 rows per head
+        assert lib.rda_attn_waves(a, a, a, a, 1, 1, 1, lq, 64, strides, 0.1, waves, None) == 1
+        assert lib.rda_attn_i8_waves(a, a, a, a, 1, 1, 1, lq, 64, strides, 0.1, waves, None) == 1
 
 
 def test_no_cpu_fallback_without_gpu(monkeypatch):

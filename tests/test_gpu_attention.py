@@ -37,11 +37,11 @@ def close(out, ref):
 
 @pytest.mark.parametrize("int8_qk", [False, True])
 # Key tiles of 32: 2, 10, 32, 1, 128, 33, 3, 5, 6 and 7 -- every count of steps the pipelined tile loop takes one at a
-# time before its six-step passes (0-5), whole and partial last tiles. Heads of 384 query rows or more take the
+# time before its six-step passes (0-5), whole and partial last tiles. Heads of 384 query rows or more also run the
 # twelve-wave workgroups (384 rows per workgroup over the (batch, head, row) range, each head's rows padded to a
-# multiple of 32): one head with padding rows (513); two whole heads; rows spanning heads with GQA 3:1 over two
-# batches and a partial last workgroup; spanning heads with GQA 2:1 and a partial last key tile; padded heads
-# spanning workgroups (400, 1000); and 1, 2, 3, 4, 5, 7, 10, 33 and 128 key tiles.
+# multiple of 32), checked bit for bit against the automatic layout: one head with padding rows (513); two whole heads;
+# rows spanning heads with GQA 3:1 over two batches and a partial last workgroup; spanning heads with GQA 2:1 and a
+# partial last key tile; padded heads spanning workgroups (400, 1000); and 1, 2, 3, 4, 5, 7, 10, 33 and 128 key tiles.
 @pytest.mark.parametrize("B,H,Hkv,Lq,Lk", [(1, 2, 2, 128, 64), (1, 2, 2, 300, 300), (2, 4, 1, 77, 1000), (1, 3, 3, 1, 5), (1, 1, 1, 513, 4096),
                                           (1, 2, 1, 200, 1049), (1, 1, 1, 64, 96), (1, 2, 2, 130, 150), (1, 1, 1, 129, 192), (2, 2, 1, 70, 210),
                                           (1, 2, 2, 384, 100), (2, 3, 1, 416, 300), (1, 4, 2, 640, 1049), (1, 3, 3, 400, 300), (2, 2, 1, 1000, 77),
@@ -54,6 +54,25 @@ def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
     hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, scale, int8_qk)
     ref = (oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64)(q.numpy(), k.numpy(), v.numpy(), scale)
     close(out, ref)
+    # Each workgroup layout that fits the shape (the automatic choice is one of them) gives the same bits.
+    for waves in (4, 12) if Lq >= 384 else (4,):
+        assert torch.equal(attention_layout(q.to(dev), k.to(dev), v.to(dev), scale, int8_qk, waves).view(torch.int16), out.view(torch.int16)), waves
+
+
+def attention_layout(q, k, v, scale, int8_qk, waves):
+    """rda_attn_waves / rda_attn_i8_waves: the attention with its workgroup layout fixed (4 or 12 waves)."""
+    lib, p = _lib.load(), _lib.ptr
+    B, H, Lq, _ = q.shape
+    _, Hkv, Lk, _ = k.shape
+    out = torch.empty_like(q)
+    strides = _lib.long_array([*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3]])
+    if int8_qk:
+        ws = torch.empty(lib.rda_attn_i8_workspace(B, Hkv, Lk), dtype=torch.uint8, device=q.device)
+        _lib.check(lib.rda_pack_k_i8(p(k), p(ws), B, Hkv, Lk, *k.stride()[:3], _lib.stream()))
+        _lib.check(lib.rda_attn_i8_waves(p(q), p(ws), p(v), p(out), B, H, Hkv, Lq, Lk, strides, scale, waves, _lib.stream()))
+    else:
+        _lib.check(lib.rda_attn_waves(p(q), p(k), p(v), p(out), B, H, Hkv, Lq, Lk, strides, scale, waves, _lib.stream()))
+    return out
 
 
 @pytest.mark.parametrize("int8_qk", [False, True])
