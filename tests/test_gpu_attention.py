@@ -59,6 +59,24 @@ def test_attention(dev, B, H, Hkv, Lq, Lk, int8_qk):
         assert torch.equal(attention_layout(q.to(dev), k.to(dev), v.to(dev), scale, int8_qk, waves).view(torch.int16), out.view(torch.int16)), waves
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_attention_random_shapes_every_layout(dev, seed):
+    """Seeded random shapes (batch 1-3, GQA 1:1-4:1, query rows 1-900, keys 1-700, fp16 and int8-QK): the automatic
+    layout within the tolerance of the float64 closed form, and every layout that fits the shape bit for bit equal to it."""
+    r = np.random.default_rng(1000 + seed)
+    B, Hkv, rep = int(r.integers(1, 4)), int(r.integers(1, 4)), int(r.choice([1, 2, 4]))
+    H, Lq, Lk, int8_qk = Hkv * rep, int(r.integers(1, 901)), int(r.integers(1, 701)), bool(seed % 2)
+    print(f"random attention B={B} H={H} Hkv={Hkv} Lq={Lq} Lk={Lk} int8_qk={int8_qk}", flush=True)
+    q, k, v = qkv(B, H, Hkv, Lq, Lk, seed=seed)
+    out = torch.empty(B, H, Lq, 128, dtype=torch.float16, device=dev)
+    scale = 128 ** -0.5
+    hip_attention.attention(q.to(dev), k.to(dev), v.to(dev), out, scale, int8_qk)
+    ref = (oracle.attention_i8qk_f64 if int8_qk else oracle.attention_f64)(q.numpy(), k.numpy(), v.numpy(), scale)
+    close(out, ref)
+    for waves in (4, 12) if Lq >= 384 else (4,):
+        assert torch.equal(attention_layout(q.to(dev), k.to(dev), v.to(dev), scale, int8_qk, waves).view(torch.int16), out.view(torch.int16)), waves
+
+
 def attention_layout(q, k, v, scale, int8_qk, waves):
     """rda_attn_waves / rda_attn_i8_waves: the attention with its workgroup layout fixed (4 or 12 waves)."""
     lib, p = _lib.load(), _lib.ptr
