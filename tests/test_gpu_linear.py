@@ -387,3 +387,30 @@ def test_linears_take_strided_activations(dev, layout):
     ws = channel_scales(N, seed=65)
     out = int8_gemm.linear(xv, w8.to(dev), ws.to(dev), None, rotate=True)
     assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w8.numpy()), s_ref, ws.numpy())))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_linears_random_shapes(dev, seed):
+    """Seeded random shapes through both linears, each against the oracle bit for bit: M from 1 to 1200 rows (partial
+    row tiles, and fewer rows than one tile), N a multiple of 64 up to 1280 (tile widths of 64 to 256, or none of them,
+    which takes the register-load GEMM), K a multiple of the rotation group up to 4096, bias on half the cases."""
+    rng = np.random.default_rng(2000 + seed)
+    M = int(rng.integers(1, 1201))
+    N = 64 * int(rng.integers(1, 21))
+    group = int(rng.choice([128, 256]))
+    K = group * int(rng.integers(1, 4096 // group + 1))
+    with_bias = bool(rng.integers(0, 2))
+    print(f"random linears seed={seed} M={M} N={N} K={K} group={group} bias={with_bias}", flush=True)
+    x = activations(M, K, seed=3000 + seed, outliers=int(rng.integers(0, 9)))
+    b = (torch.randn(N, generator=gen(3100 + seed)) * 0.5).half() if with_bias else None
+    bd = None if b is None else b.to(dev)
+    bn = None if b is None else b.numpy()
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), group=group)
+    w8 = int8_weights(N, K, seed=3200 + seed)
+    ws = channel_scales(N, seed=3300 + seed)
+    out = int8_gemm.linear(x.to(dev), w8.to(dev), ws.to(dev), bd, rotate=True, group=group)
+    assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w8.numpy()), s_ref, ws.numpy(), bn)))
+    w, wp = int4_weights(N, K, seed=3400 + seed)
+    gs = (torch.rand(N, K // 128, generator=gen(3500 + seed)) * 1.5e-2 + 5e-3).half()
+    out = int8_gemm.linear_w4a8(x.to(dev), wp.to(dev), gs.to(dev), bd, group=group)
+    assert_same(bits(out), bits(oracle.w4a8_epilogue(oracle.w4a8_partials(q_ref, w.numpy()), s_ref, gs.numpy(), bn)))
