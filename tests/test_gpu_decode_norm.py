@@ -140,6 +140,29 @@ def test_attention_decode(dev, B, H, Hkv, cap, lengths):
     assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_attention_decode_random_shapes(dev, seed):
+    """Seeded random caches: batch 1-4, 1-8 KV heads with 1, 2, 4 or 8 query heads each, capacity 1-2600 and a ragged
+    length per batch row in [1, capacity] (the last row's at capacity on even seeds), against float64."""
+    rng = np.random.default_rng(4000 + seed)
+    B = int(rng.integers(1, 5))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    H = Hkv * int(rng.choice([1, 2, 4, 8]))
+    cap = int(rng.integers(1, 2601))
+    lengths = [int(n) for n in rng.integers(1, cap + 1, size=B)]
+    if seed % 2 == 0:
+        lengths[-1] = cap
+    print(f"attention_decode random seed={seed} B={B} H={H} Hkv={Hkv} cap={cap} lengths={lengths}", flush=True)
+    g = gen(4100 + seed)
+    q = torch.randn(B, 1, H, 128, generator=g).float()
+    k = torch.randn(B, cap, Hkv, 128, generator=g).float()
+    v = torch.randn(B, cap, Hkv, 128, generator=g).float()
+    out = int8_gemv.attention_decode(q.to(dev), k.to(dev), v.to(dev), torch.tensor(lengths, dtype=torch.int32).to(dev))
+    ref = oracle.attention_decode_f64(q.numpy(), k.numpy(), v.numpy(), lengths)
+    err = np.abs(out.cpu().double().numpy() - ref)
+    assert np.all(err <= 1e-5 + 1e-4 * np.abs(ref)), f"max err {err.max():.3e}"
+
+
 def test_attention_decode_length_past_capacity(dev):
     """A length past the cache's capacity reads no row beyond it: the kernel takes it as the capacity, bit for bit."""
     g = gen(23)
