@@ -121,6 +121,64 @@ def test_rot_quant_i4_bit_exact(dev, M, K):
     assert_same(q, q_ref)
 
 
+QUANT_KINDS = ["plain", "rot", "i4", "swiglu", "gate", "situ", "mod"]
+
+
+@pytest.mark.parametrize("seed", range(14))
+def test_quantizers_random_shapes(dev, seed):
+    """Seeded random shapes through every activation quantizer, codes and scales bit for bit against the oracle: M
+    from 1 to 600 rows; K a multiple of the rotation group (128 or 256) up to the 16384 values a row keeps in LDS
+    (MOD: up to 8192, group 256); plain quantization K a multiple of 16 up to 25600 (past 16384 the row is read
+    again, not staged); an all-zero row where there are two rows or more."""
+    kind = QUANT_KINDS[seed % len(QUANT_KINDS)]
+    rng = np.random.default_rng(5000 + seed)
+    M = int(rng.integers(1, 601))
+    group = 256 if kind == "mod" else int(rng.choice([128, 256]))
+    K = (16 * int(rng.integers(1, 1601)) if kind == "plain" else 256 * int(rng.integers(1, 33)) if kind == "mod"
+         else group * int(rng.integers(1, 16384 // group + 1)))
+    print(f"random quantizer seed={seed} {kind} M={M} K={K} group={group}", flush=True)
+    g = gen(5100 + seed)
+    k = kern()
+    if kind in ("plain", "rot", "i4"):
+        x = activations(M, K, seed=5200 + seed, outliers=int(rng.integers(0, 9)))
+        if M >= 2:
+            x[int(rng.integers(0, M))] = 0
+        if kind == "plain":
+            packed, scale = int8_gemm.quantize(k.quant_pack_a, x.to(dev), K)
+            q_ref, s_ref = oracle.quant_rows(x.numpy())
+        else:
+            entry = k.rot_quant_pack_a if kind == "rot" else k.rot_quant_pack_a_i4
+            packed, scale = int8_gemm.quantize(entry, x.to(dev), K, group=group)
+            q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), group=group, i4=kind == "i4")
+    elif kind == "situ":
+        x = (torch.randn(M, 2 * K, generator=g) * 3).half()
+        packed, scale = int8_gemm.quantize(k.situ_rot_quant_pack_a, x.to(dev), K, group=group)
+        q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), act=oracle.ACT_SITU, group=group)
+    elif kind in ("swiglu", "gate"):
+        a = (torch.randn(M, K, generator=g) * 4).half()
+        b = (torch.randn(M, K, generator=g) * 4).half()
+        entry = k.swiglu_rot_quant_pack_a if kind == "swiglu" else k.gate_rot_quant_pack_a
+        packed, scale = int8_gemm.quantize(entry, a.to(dev), K, up=b.to(dev), group=group)
+        q_ref, s_ref, _ = oracle.rot_quant_rows(a.numpy(), act=oracle.ACT_SWIGLU if kind == "swiglu" else oracle.ACT_GATE, group=group,
+                                                u=b.numpy())
+    else:
+        L = int(rng.integers(1, M + 1))
+        while M % L:
+            L -= 1
+        B = M // L
+        x = torch.randn(M, K, generator=g).half()
+        w = (torch.randn(K, generator=g) * 0.1).float()
+        sm = (1 + torch.randn(B, K, generator=g) * 0.2).half()
+        t = (torch.randn(B, K, generator=g) * 0.2).half()
+        packed, scale = int8_gemm.quantized(M, K, dev)
+        p = int8_gemm._lib.ptr
+        xd, wd, sd, td = x.to(dev), w.to(dev), sm.to(dev), t.to(dev)
+        int8_gemm.launch(k.mod_rot_quant_pack_a, 0, 0, 0, [p(xd), p(packed), p(scale), M, K, p(wd), p(sd), p(td), L, 1e-6])
+        q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), act=oracle.ACT_MOD, mod=(w.numpy(), sm.numpy(), t.numpy(), L, 1e-6))
+    assert_same(scale.cpu().numpy(), s_ref)
+    assert_same(q_of(packed, M, K), q_ref)
+
+
 def packed_from(a_int8):
     return torch.from_numpy(np.ascontiguousarray(a_int8)).view(torch.int32).reshape(-1)
 
