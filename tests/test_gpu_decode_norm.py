@@ -88,6 +88,55 @@ def test_rotate_gemv_i8_bit_exact(dev, N, K, group):
     assert np.all(np.abs(out.cpu().double().numpy().reshape(-1) - f64) <= gemv_bound(w.numpy(), xr, s.numpy(), False))
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_gemvs_random_shapes(dev, seed):
+    """Seeded random shapes through the decode GEMVs: N from 1 to 6000 rows (split K, one row per wave, and the 16-wave
+    workgroups past K = 8192), K a multiple of 512 up to 16384, fp32 or fp16 x, bias on half the cases. gemv within
+    its bound of float64; rotate_gemv (a random rotation group) == rotate then gemv bit for bit, its stored rotation the
+    oracle's; for K <= 8192, gemv_multi over 1-4 matrices of random heights == one launch per matrix bit for bit."""
+    rng = np.random.default_rng(6000 + seed)
+    N = int(rng.integers(1, 6001))
+    K = 512 * int(rng.integers(1, 33))
+    x_half = bool(rng.integers(0, 2))
+    group = int(rng.choice(int8_gemv.FUSED_ROTATION_GROUPS))
+    with_bias = bool(rng.integers(0, 2))
+    print(f"random gemvs seed={seed} N={N} K={K} half={x_half} group={group} bias={with_bias}", flush=True)
+    x = torch.randn(1, K, generator=gen(6100 + seed))
+    w = int8_weights(N, K, seed=6200 + seed)
+    sc = channel_scales(N, seed=6300 + seed)
+    b = torch.randn(N, generator=gen(6400 + seed)).float() if with_bias else None
+    wd, sd, bd = w.to(dev), sc.to(dev), None if b is None else b.to(dev)
+    bn = None if b is None else b.numpy()
+    xv = x.half() if x_half else x.float()
+    out = int8_gemv.gemv(xv.to(dev), wd, sd, bd)
+    xf = xv.float().numpy().reshape(-1)
+    ref = oracle.gemv_f64(xf, w.numpy(), sc.numpy(), bn)
+    bound = gemv_bound(w.numpy(), xf, sc.numpy(), x_half) + (np.abs(ref) * 2.0 ** -10 if x_half else 0)
+    err = np.abs(out.cpu().double().numpy().reshape(-1) - ref)
+    assert np.all(err <= bound), f"gemv: max err {err.max():.3e}"
+
+    xd = x.float().to(dev)
+    kept = torch.full_like(xd, float("nan"))
+    fused = int8_gemv.rotate_gemv(xd, group, wd, sd, bd, kept)
+    rotated = int8_gemv.rotate(xd, group)
+    assert_same(fused.cpu().numpy(), int8_gemv.gemv(rotated, wd, sd, bd).cpu().numpy())
+    assert_same(kept.cpu().numpy(), oracle.rotate_f32(x.float().numpy().reshape(-1, group), group).reshape(1, K), "stored rotation")
+
+    if K <= 8192:
+        layers = [(wd, sd, bd)]
+        for i in range(int(rng.integers(0, 4))):
+            n = int(rng.integers(1, 6001))
+            layers.append((int8_weights(n, K, seed=6500 + 10 * seed + i).to(dev), channel_scales(n, seed=6600 + 10 * seed + i).to(dev),
+                           torch.randn(n, generator=gen(6700 + 10 * seed + i)).float().to(dev) if rng.integers(0, 2) else None))
+        mgroup = int(rng.choice([0, group]))
+        xm = xd if mgroup else xv.to(dev)
+        print(f"  gemv_multi heights={[l[0].shape[0] for l in layers]} group={mgroup}", flush=True)
+        outs = int8_gemv.gemv_multi(xm, layers, group=mgroup)
+        for o, (lw, ls, lb) in zip(outs, layers):
+            one = int8_gemv.rotate_gemv(xm, mgroup, lw, ls, lb) if mgroup else int8_gemv.gemv(xm, lw, ls, lb)
+            assert_same(o.cpu().numpy(), one.cpu().numpy())
+
+
 @pytest.mark.parametrize("half", [False, True])
 def test_gemv_unaligned_view(dev, half):
     """An input view one element into its storage (taken through an aligned copy): within the bound of the others."""
