@@ -268,3 +268,35 @@ def test_rms_norm_rope_bit_exact(dev, fb):
     f = freqs.numpy() if fb > 1 else np.broadcast_to(freqs.numpy(), (B,) + freqs.shape[1:])
     ref = oracle.rms_norm(xh, w.numpy(), 1e-6, freqs=np.ascontiguousarray(f))
     assert_same(bits(out), bits(ref))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_norms_random_shapes(dev, seed):
+    """Seeded random shapes, bit for bit against the oracle: RMSNorm of (B, L, D) or (B, H, L, D) (up to 1 x 600, 4 x 300,
+    3 x 5 x 200 rows) and D a multiple of 8 up to 8192, eps 1e-6 or 1e-5; QK-norm + RoPE of B = 1-3, L = 1-700 and 1-24 heads, read
+    from the q, k or v third of a fused (B, L, 3 H 128) buffer, with one set of rotations or one per batch row."""
+    rng = np.random.default_rng(7000 + seed)
+    g = gen(7100 + seed)
+    caps = {1: [1, 600], 2: [4, 300], 3: [3, 5, 200]}[int(rng.integers(1, 4))]  # (B, L, D) or (B, H, L, D)
+    lead = [int(rng.integers(1, c + 1)) for c in caps]
+    D = 8 * int(rng.integers(1, 1025))
+    eps = float(rng.choice([1e-6, 1e-5]))
+    print(f"random norms seed={seed} rms_norm {(*lead, D)} eps={eps}", flush=True)
+    x = torch.randn(*lead, D, generator=g).half()
+    w = (torch.randn(D, generator=g) * 0.1).float()
+    out = rms_norm.rms_norm(x.to(dev), w.to(dev), eps)
+    assert_same(bits(out), bits(oracle.rms_norm(x.numpy(), w.numpy(), eps)))
+
+    B, L, H = int(rng.integers(1, 4)), int(rng.integers(1, 701)), int(rng.integers(1, 25))
+    fb = int(rng.choice([1, B]))
+    third = int(rng.integers(0, 3))
+    print(f"  rms_norm_rope B={B} L={L} H={H} freq batches={fb} third={third}", flush=True)
+    fused = torch.randn(B, L, 3 * H * 128, generator=g).half()
+    w = (torch.randn(128, generator=g) * 0.1).float()
+    ang = torch.randn(fb, 1, L, 64, generator=g) * 3
+    freqs = torch.stack([torch.cos(ang), -torch.sin(ang), torch.sin(ang), torch.cos(ang)], -1).reshape(fb, 1, L, 64, 2, 2).float()
+    view = fused.to(dev)[:, :, third * H * 128:(third + 1) * H * 128]
+    out = rms_norm.rms_norm_rope(view, H, _Norm(w.to(dev), eps), freqs.to(dev))
+    xh = fused[:, :, third * H * 128:(third + 1) * H * 128].reshape(B, L, H, 128).transpose(1, 2).contiguous().numpy()
+    f = freqs.numpy() if fb > 1 else np.broadcast_to(freqs.numpy(), (B,) + freqs.shape[1:])
+    assert_same(bits(out), bits(oracle.rms_norm(xh, w.numpy(), eps, freqs=np.ascontiguousarray(f))))
