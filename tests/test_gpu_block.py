@@ -87,3 +87,29 @@ def test_block_forward_matches_oracle_chain(dev, hooked, B, L, D, heads, hidden,
     ref = oracle_block(blk, x, freqs, gpu_attention)
     assert_same(bits(out), bits(ref))
 
+
+@pytest.mark.parametrize("seed", range(6))
+def test_block_forward_random_shapes(dev, hooked, seed):
+    """Seeded random block shapes, bit for bit against the oracle's chain: B 1 or 2, L with B L >= 512 (the fused path's
+    minimum) up to 900 tokens, 2, 4 or 6 heads, an MLP width a multiple of 256 up to 2048; int8 QK^T on odd seeds."""
+    rng = np.random.default_rng(8000 + seed)
+    B = 2 if seed % 3 == 2 else 1
+    L = int(rng.integers(-(-512 // B), 901))
+    heads = int(rng.choice([2, 4, 6]))
+    D, hidden = heads * 128, 256 * int(rng.integers(1, 9))
+    int8_qk = bool(seed % 2)
+    print(f"block_forward random seed={seed} B={B} L={L} D={D} heads={heads} hidden={hidden} int8_qk={int8_qk}", flush=True)
+    blk = fakes.make_krea2_block(hooked, D, heads, hidden, B, dev, seed=8100 + seed)
+    x = torch.randn(B, L, D, generator=gen(8200 + seed)).half()
+    freqs = freqs_for(L, 8300 + seed)
+    xd, fd = x.to(dev), freqs.to(dev)
+    assert int8_gemm._block_fusable(blk, xd, fd, None, None, {}), "the shape must take the fused path"
+    out = int8_gemm.block_forward(blk, int8_qk, xd, None, fd)
+
+    def gpu_attention(q, k, v):
+        qt, kt, vt = (torch.from_numpy(np.ascontiguousarray(t)).to(dev) for t in (q, k, v))
+        o = torch.empty_like(qt)
+        hip_attention.attention(qt, kt, vt, o, 128 ** -0.5, int8_qk)
+        return o.cpu().numpy()
+
+    assert_same(bits(out), bits(oracle_block(blk, x, freqs, gpu_attention)))
