@@ -121,6 +121,38 @@ def test_rot_quant_i4_bit_exact(dev, M, K):
     assert_same(q, q_ref)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_w4a4_and_residual_random_shapes(dev, seed):
+    """Seeded random shapes, bit for bit against the oracle: the W4A4 hook pair (rot_quant_pack_a_i4 + gemm_i4; M 1-1200,
+    N a multiple of 64 up to 1280, K a multiple of 256 up to 4096) and the W8A8 linear with the block's gated residual
+    in its epilogue (B 1-3 rows of L 1-600 tokens, N a multiple of 64 up to 1280, K a multiple of 256 up to 4096)."""
+    rng = np.random.default_rng(9000 + seed)
+    M, N, K = int(rng.integers(1, 1201)), 64 * int(rng.integers(1, 21)), 256 * int(rng.integers(1, 17))
+    print(f"random w4a4 seed={seed} M={M} N={N} K={K}", flush=True)
+    x = activations(M, K, seed=9100 + seed)
+    w, wp = int4_weights(N, K, seed=9200 + seed)
+    ws = channel_scales(N, seed=9300 + seed)
+    k = kern()
+    out = int8_gemm.run(k.rot_quant_pack_a_i4, k.gemm_i4, x.to(dev), wp.to(dev), ws.to(dev), None, K)
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy(), i4=True)
+    assert_same(bits(out), bits(oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w.numpy()), s_ref, ws.numpy())))
+
+    B, L = int(rng.integers(1, 4)), int(rng.integers(1, 601))
+    N, K = 64 * int(rng.integers(1, 21)), 256 * int(rng.integers(1, 17))
+    M = B * L
+    print(f"  residual epilogue B={B} L={L} K={K} N={N}", flush=True)
+    g = gen(9400 + seed)
+    x = activations(M, K, seed=9500 + seed)
+    w8 = int8_weights(N, K, seed=9600 + seed)
+    ws = channel_scales(N, seed=9700 + seed)
+    R = torch.randn(B, L, N, generator=g).half()
+    G = torch.randn(B, N, generator=g).half()
+    out = int8_gemm.linear(x.to(dev), w8.to(dev), ws.to(dev), None, rotate=True, res=(R.to(dev), G.to(dev)))
+    q_ref, s_ref, _ = oracle.rot_quant_rows(x.numpy())
+    ref = oracle.gemm_epilogue(oracle.gemm_acc(q_ref, w8.numpy()), s_ref, ws.numpy(), R=R.numpy().reshape(M, N), G=G.numpy(), L=L)
+    assert_same(bits(out), bits(ref))
+
+
 QUANT_KINDS = ["plain", "rot", "i4", "swiglu", "gate", "situ", "mod"]
 
 
